@@ -1,0 +1,254 @@
+"""Benchmark of the MLP training step on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-bwd]
+
+Workload (one "step"): MLP 512->1024(ReLU)->1024(ReLU)->10, f32, batch 2048,
+softmax cross-entropy, Adam(1e-3, 0.9, 0.999, 1e-8): forward, backward and the
+optimizer update, on synthetic N(0,1) batches with uniform labels in [0,10)
+that are resident in HBM before timing starts (one fresh batch per step).
+
+Prints ONE JSON line.  `value` is ms/step over K timed steps (lower is
+better).  Next to it:
+  roofline      the dominant kernel of the step: algorithmic FLOPs per launch
+                over its average HIP-event duration, against the f32 MFMA peak
+  bwd_gemm      Linear 4096->4096 backward at batch 8192 in bf16 (dX = dY·Wᵀ,
+                dW = Xᵀ·dY with db fused), TFLOP/s against the bf16 MFMA peak
+  cpu_baseline  the CPU oracle (C++ restatement of rtensor's single-threaded
+                CPU path) timed on a bounded sample of the same workload
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_F32_TFLOPS = 157.3   # MI355X dense f32 matrix
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 matrix
+PEAK_HBM_GBS = 8000.0
+REF_GPU_MS_B2048 = 6.89   # rtensor GPU step at batch 2048 (README.md:53), RTX 4070 Laptop
+
+DIMS = [512, 1024, 1024, 10]
+BATCH = 2048
+
+
+def kaiming(rng, fan_in, fan_out):
+    bound = np.sqrt(6.0 / fan_in)
+    return rng.uniform(-bound, bound, size=(fan_in, fan_out)).astype(np.float32)
+
+
+def step_flops(dims, batch):
+    """Algorithmic FLOPs of one step: forward + dW per layer + dX for layers > 0."""
+    f = 0
+    for l in range(len(dims) - 1):
+        mk = dims[l] * dims[l + 1]
+        f += 2 * batch * mk * (3 if l > 0 else 2)
+    return f
+
+
+def label_flops(label, dims, batch):
+    """FLOPs per launch of a plan kernel label (fwd_l*, dw_l*, dx_l*)."""
+    for pre in ("fwd_l", "dw_l", "dx_l"):
+        if label.startswith(pre):
+            l = int(label[len(pre):])
+            return 2 * batch * dims[l] * dims[l + 1]
+    return 0
+
+
+def traffic_for(label):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
+    from the committed summary profiles/pmc_traffic.json, if present."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(label, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_step(gpu, G, steps, warmup):
+    rng = np.random.default_rng(2048)
+    params = []
+    for l in range(len(DIMS) - 1):
+        params += [kaiming(rng, DIMS[l], DIMS[l + 1]), np.zeros((1, DIMS[l + 1]), np.float32)]
+    mlp = G.GpuMlp.from_params(gpu, params, BATCH, 1e-3)
+    nb = min(steps + warmup, 64)
+    xs = [gpu.upload(rng.standard_normal((BATCH, DIMS[0]), dtype=np.float32)) for _ in range(nb)]
+    ys = [G.upload_labels(gpu, rng.integers(0, DIMS[-1], BATCH)) for _ in range(nb)]
+    gpu.sync()
+    for i in range(warmup):
+        mlp.step(xs[i % nb], ys[i % nb])
+    gpu.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        mlp.step(xs[(warmup + i) % nb], ys[(warmup + i) % nb])
+    gpu.sync()
+    wall = time.perf_counter() - t0
+    loss = mlp.last_loss()
+
+    # Second pass of the same steps with HIP events around every launch (on
+    # the library's stream) for per-kernel durations.
+    gpu.profile_reset()
+    gpu.profile(True)
+    for i in range(steps):
+        mlp.step(xs[(warmup + i) % nb], ys[(warmup + i) % nb])
+    gpu.sync()
+    gpu.profile(False)
+    prof = gpu.perfilar()
+    gpu.profile_reset()
+    return wall, loss, prof, mlp.dispatches_por_passo()
+
+
+def bench_bwd_gemm(gpu, G, reps=20):
+    """Linear 4096->4096 backward at batch 8192, bf16 operands, f32 accumulate."""
+    B, D = 8192, 4096
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((B, D), dtype=np.float32) / np.float32(64.0))
+    dy = (rng.standard_normal((B, D), dtype=np.float32) / np.float32(64.0))
+    w = rng.uniform(-np.sqrt(6.0 / D), np.sqrt(6.0 / D), size=(D, D)).astype(np.float32)
+    gx, gdy, gw = gpu.upload(x, G.BF16), gpu.upload(dy, G.BF16), gpu.upload(w, G.BF16)
+    dx = gpu.zeros((B, D), G.BF16)
+    dw = gpu.zeros((D, D), G.F32)
+    db = gpu.zeros((1, D), G.F32)
+    for _ in range(3):
+        gpu.gemm(G.NT, gdy, gw, dx)
+        gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
+    gpu.sync()
+    gpu.profile_reset()
+    gpu.profile(True)
+    for _ in range(reps):
+        gpu.gemm(G.NT, gdy, gw, dx)
+    for _ in range(reps):
+        gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
+    gpu.sync()
+    gpu.profile(False)
+    prof = {n: ms / c for n, c, ms in gpu.perfilar()}
+    gpu.profile_reset()
+    flops = 2.0 * B * D * D
+    t_dx, t_dw = prof["gemm_nt"], prof["gemm_tn"]
+    tf_dx = flops / (t_dx * 1e-3) / 1e12
+    tf_dw = flops / (t_dw * 1e-3) / 1e12
+    tf = 2 * flops / ((t_dx + t_dw) * 1e-3) / 1e12
+    return {
+        "config": "Linear 4096->4096 backward, batch 8192, bf16 in / f32 accumulate; dX bf16, dW f32, db fused",
+        "dX_ms": round(t_dx, 4), "dW_db_ms": round(t_dw, 4),
+        "dX_tflops": round(tf_dx, 1), "dW_tflops": round(tf_dw, 1),
+        "tflops": round(tf, 1), "peak_tflops": PEAK_BF16_TFLOPS, "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+    }
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle's single-threaded training step on the host, bounded sample."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    rng = np.random.default_rng(7)
+    params = []
+    for l in range(len(DIMS) - 1):
+        params += [kaiming(rng, DIMS[l], DIMS[l + 1]), np.zeros((1, DIMS[l + 1]), np.float32)]
+    m = O.CpuMlp(params[0::2], params[1::2])
+    m.set_optimizer("adam", 1e-3)
+    x = rng.standard_normal((BATCH, DIMS[0]), dtype=np.float32)
+    y = rng.integers(0, DIMS[-1], BATCH).astype(np.uint32)
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        m.step(x, y)
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 20:
+            break
+    ms = (time.perf_counter() - t0) / n * 1e3
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(ms, 2), "unit": "ms/step", "cores": 1, "kind": "port",
+            "sample": f"{n} steps of the batch-2048 Adam step, oracle C++ port of rtensor's CPU path, "
+                      f"1 thread on {cpu} ({os.cpu_count()} logical CPUs visible)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-bwd", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the data-parallel "
+              "all-reduce is not built).", file=sys.stderr)
+        sys.exit(2)
+
+    from rgpu_amd import gpu as G
+
+    gpu = G.Gpu(0)
+    wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
+    ms = wall / args.steps * 1e3
+    total_flops = step_flops(DIMS, BATCH)
+
+    kernels = {}
+    dom = None
+    for name, count, tot in prof:
+        avg = tot / count
+        kernels[name] = round(avg * 1e3, 2)  # µs per launch
+        if dom is None or tot > dom[2]:
+            dom = (name, count, tot)
+    name, count, tot = dom
+    avg_ms = tot / count
+    flops = label_flops(name, DIMS, BATCH)
+    if flops:
+        achieved = flops / (avg_ms * 1e-3) / 1e12
+        roof = {"kernel": name, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_F32_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_TFLOPS, 4), "traffic": traffic_for(name),
+                "flops_per_launch": flops, "avg_us": round(avg_ms * 1e3, 2)}
+    else:
+        roof = {"kernel": name, "bound": "hbm", "achieved": None, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": None, "traffic": traffic_for(name), "avg_us": round(avg_ms * 1e3, 2)}
+
+    out = {
+        "metric": "ms/step MLP 512-1024-1024-10 train @B=2048; bwd GEMM TFLOP/s % of peak",
+        "value": round(ms, 4),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(ms / REF_GPU_MS_B2048, 4),
+        "vs_baseline_ref": "rtensor wgpu step 6.89 ms at batch 2048 on an RTX 4070 Laptop (README.md:53)",
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "MLP 512-1024(ReLU)-1024(ReLU)-10 softmax-xent train step, f32, Adam",
+                   "global_batch": BATCH, "dims": DIMS, "optimizer": "adam(1e-3,0.9,0.999,1e-8)",
+                   "parallelism": "single GPU"},
+        "step_tflops": round(total_flops / (ms * 1e-3) / 1e12, 2),
+        "launches_per_step": launches,
+        "final_loss": round(float(loss), 5),
+        "roofline": roof,
+        "kernels_us": kernels,
+    }
+    if not args.no_bwd:
+        out["bwd_gemm"] = bench_bwd_gemm(gpu, G)
+    if not args.no_cpu:
+        cb = cpu_baseline()
+        out["cpu_baseline"] = cb
+        out["speedup_vs_cpu"] = round(cb["value"] / ms, 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

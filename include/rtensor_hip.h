@@ -1,0 +1,198 @@
+/*
+ * rtensor_hip.h -- C ABI of the MI355X (gfx950) training backend for rtensor.
+ *
+ * The backend replaces rtensor's wgpu module (crates/rtensor/src/gpu/mod.rs)
+ * for the MLP training step.  Each entry point below names the rtensor::gpu
+ * call it stands in for (file:line in the rtensor crate).  A Rust FFI crate
+ * binds these symbols one-for-one; see INTEGRATION.md for the binding.
+ *
+ * Conventions
+ *   - Every function returns an int status (rt_status); 0 is success.  The
+ *     reference panics on misuse (mod.rs:1342-1343, 1487-1491, 799); here the
+ *     same conditions return RT_ERR_SHAPE / RT_ERR_INVALID / RT_ERR_LABEL and
+ *     leave a message in rt_last_error(ctx).
+ *   - Host memory is caller-owned: the library never keeps a host pointer
+ *     past the call and never calls back.
+ *   - One HIP stream per rt_ctx.  Kernel entry points only enqueue work, like
+ *     Gpu::record + Gpu::submit (mod.rs:609, 1231-1237); rt_download,
+ *     rt_sync and the rt_mlp_* readers block, like Gpu::download
+ *     (mod.rs:530-544).  An rt_ctx is not thread-safe, as Gpu is not Send.
+ *   - Tensors are dense row-major.  Weights are [in, out], biases [1, out],
+ *     parameters travel in the order [W1, b1, W2, b2, ...] (nn.rs:190-192).
+ *     Labels are u32 (mod.rs:1672-1675).
+ */
+#ifndef RTENSOR_HIP_H
+#define RTENSOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct rt_ctx rt_ctx; /* ~ rtensor::gpu::Gpu        (mod.rs:224-255)   */
+typedef struct rt_buf rt_buf; /* ~ rtensor::gpu::GpuTensor  (mod.rs:190-208)   */
+typedef struct rt_mlp rt_mlp; /* ~ rtensor::gpu::GpuMlp     (mod.rs:1322-1336) */
+
+typedef enum {
+  RT_OK = 0,
+  RT_ERR_NO_DEVICE = 1,   /* Gpu::new() -> Err (mod.rs:263-277)             */
+  RT_ERR_INVALID = 2,     /* null handle, bad enum, bad size                 */
+  RT_ERR_SHAPE = 3,       /* the reference's shape assert! (mod.rs:1487-1491) */
+  RT_ERR_DTYPE = 4,       /* operand dtype not supported by the entry point  */
+  RT_ERR_OOM = 5,         /* device allocation failed                        */
+  RT_ERR_LABEL = 6,       /* a label >= number of classes (undefined in the
+                             reference's xent kernel, kernels.rs:158-159)    */
+  RT_ERR_HIP = 7,         /* a HIP runtime call failed                       */
+  RT_ERR_OVERFLOW = 8     /* non-finite gradient under loss scaling          */
+} rt_status;
+
+typedef enum { RT_F32 = 0, RT_BF16 = 1, RT_F16 = 2, RT_U32 = 3 } rt_dtype;
+
+/* C = A·B, Aᵀ·B (A stored [K, M]) or A·Bᵀ (B stored [N, K]). */
+typedef enum { RT_NN = 0, RT_TN = 1, RT_NT = 2 } rt_layout;
+
+typedef enum {
+  RT_EPI_NONE = 0,      /* C = acc                                           */
+  RT_EPI_BIAS = 1,      /* C = acc + 1ₙb               (mm_bias, gemm.rs:452) */
+  RT_EPI_BIAS_RELU = 2, /* C = max(acc + 1ₙb, 0)       (flag_relu, gemm.rs:389) */
+  RT_EPI_RELU_MASK = 3  /* C = acc ⊙ 1[aux > 0]        (relu_bwd, kernels.rs:119) */
+} rt_epilogue;
+
+/* ------------------------------------------------------------- device */
+
+/* Gpu::new / Gpu::with_preference (mod.rs:263-277).  device = HIP ordinal. */
+int rt_open(int device, rt_ctx** out);
+int rt_close(rt_ctx* ctx);
+/* Message for the last failed call on ctx (or of rt_open when ctx is NULL). */
+const char* rt_last_error(const rt_ctx* ctx);
+/* Gpu::info (mod.rs:412): device name and arch, NUL-terminated into buf. */
+int rt_info(rt_ctx* ctx, char* buf, size_t len);
+/* Gpu::sync (mod.rs:564-566): wait for all enqueued work.  Returns
+ * RT_ERR_LABEL (once) if a softmax-xent launch saw a label >= classes. */
+int rt_sync(rt_ctx* ctx);
+
+/* ------------------------------------------------------------- buffers */
+
+/* Gpu::zeros (mod.rs:501-506). rank <= 4. */
+int rt_zeros(rt_ctx* ctx, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out);
+/* Gpu::upload (mod.rs:509-517); host holds prod(shape) elements of dtype. */
+int rt_upload(rt_ctx* ctx, rt_dtype dtype, const size_t* shape, int rank, const void* host, rt_buf** out);
+/* Gpu::download (mod.rs:530-544): blocking copy of the whole tensor;
+ * bytes must equal the tensor's size in bytes. */
+int rt_download(rt_ctx* ctx, const rt_buf* buf, void* host, size_t bytes);
+/* Asynchronous host->device overwrite of an existing buffer (the plan's
+ * per-step writes, mod.rs:1486-1495). */
+int rt_write(rt_ctx* ctx, rt_buf* buf, const void* host, size_t bytes);
+int rt_free(rt_ctx* ctx, rt_buf* buf);
+/* GpuTensor::shape / len (mod.rs:197-208).  shape needs room for 4. */
+int rt_buf_info(const rt_buf* buf, rt_dtype* dtype, size_t* shape, int* rank);
+/* upload_labels (mod.rs:1672-1675): usize labels -> u32 device buffer. */
+int rt_upload_labels(rt_ctx* ctx, const uint64_t* labels, size_t n, rt_buf** out);
+/* f32 -> bf16/f16 with round-to-nearest-even, or half -> f32 (same shape):
+ * upload_f16 / op_empacota_f16 (mod.rs:1151-1185, EMPACOTA mista.rs:326-341). */
+int rt_convert(rt_ctx* ctx, const rt_buf* src, rt_buf* dst);
+
+/* ------------------------------------------------------------- ops */
+
+/* GEMM with f32 accumulate.  op_matmul / op_matmul_at_b / op_matmul_a_bt
+ * (mod.rs:685-700), op_matmul_bias (mod.rs:722-749) and op_matmul_f16
+ * (mod.rs:1191-1229).  A and B are both f32, both bf16 or both f16; C is
+ * f32, or bf16 for half inputs.  aux is the bias [1, N] for RT_EPI_BIAS*,
+ * or the mask source [M, N] for RT_EPI_RELU_MASK, else NULL.  colsum, if not
+ * NULL, receives f32 column sums of B over K (= 1ᵀ·B, the bias gradient when
+ * B is δ): supported for RT_TN. */
+int rt_gemm(rt_ctx* ctx, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* c,
+            rt_epilogue epi, const rt_buf* aux, rt_buf* colsum);
+
+/* ops_split_k (mod.rs:1095-1146): C = A·B (RT_NN) or Aᵀ·B (RT_TN) with K cut
+ * into `slices`; slice s writes partials[s] and a fixed-order reduction sums
+ * them (deterministic, no atomics).  partials is f32 with >= slices*M*N
+ * elements.  colsum as in rt_gemm (RT_TN only). */
+int rt_gemm_splitk(rt_ctx* ctx, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* c,
+                   rt_buf* partials, size_t slices, rt_buf* colsum);
+/* fatias_sugeridas (mod.rs:1079-1088), re-derived for 256 CUs. */
+size_t rt_splitk_slices(size_t m, size_t n, size_t k);
+
+/* ops_colsum (mod.rs:838-855): dst[1, C] (f32) = 1ᵀ·src[R, C] (f32/bf16/f16). */
+int rt_colsum(rt_ctx* ctx, const rt_buf* src, rt_buf* dst);
+/* op_bias_add (mod.rs:752-762): Z += 1ₙb in place. */
+int rt_bias_add(rt_ctx* ctx, rt_buf* z, const rt_buf* b);
+/* op_relu (mod.rs:765-775): Y = max(X, 0). */
+int rt_relu(rt_ctx* ctx, const rt_buf* x, rt_buf* y);
+/* op_relu_bwd (mod.rs:778-788): δ ← δ ⊙ 1[A > 0] in place. */
+int rt_relu_bwd(rt_ctx* ctx, const rt_buf* a, rt_buf* delta);
+/* op_softmax_xent (mod.rs:791-808): per row loss -ln(max(p_y, 1e-12)) into
+ * loss_rows[B] and δ = (softmax(z) - onehot(y)) * (scale / B).  Labels >= C
+ * are reported by the next blocking call as RT_ERR_LABEL. */
+int rt_softmax_xent(rt_ctx* ctx, const rt_buf* logits, const rt_buf* labels, rt_buf* delta,
+                    rt_buf* loss_rows, float scale);
+/* op_adam + atualizar_adam (mod.rs:859-907) with Adam::step's arithmetic
+ * (optim.rs:162-198): t is the 1-based step that sets c1 = 1-β1^t, c2 = 1-β2^t. */
+int rt_adam(rt_ctx* ctx, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, float lr, float beta1,
+            float beta2, float eps, int t);
+/* Sgd::step (optim.rs:80-114); velocity may be NULL when momentum == 0. */
+int rt_sgd(rt_ctx* ctx, rt_buf* theta, rt_buf* velocity, const rt_buf* g, float lr, float momentum);
+
+/* ------------------------------------------------------------- model */
+
+typedef enum { RT_OPT_ADAM = 0, RT_OPT_SGD = 1 } rt_optimizer;
+typedef enum { RT_PREC_F32 = 0, RT_PREC_BF16 = 1 } rt_precision;
+
+typedef struct {
+  int optimizer;    /* rt_optimizer                                      */
+  float lr;         /* GpuMlp::from_params lr (mod.rs:1341)              */
+  float beta1;      /* 0.9   (mod.rs:1462)                               */
+  float beta2;      /* 0.999                                            */
+  float eps;        /* 1e-8  (mod.rs:873)                                */
+  float momentum;   /* Sgd momentum (optim.rs:96-100)                    */
+  int precision;    /* rt_precision: bf16 weights/activations with f32
+                       master weights when RT_PREC_BF16                 */
+  float loss_scale; /* static loss scale (RT_PREC_BF16), 1 = none       */
+} rt_mlp_config;
+
+/* GpuMlp::from_params (mod.rs:1341-1482).  n_layers Dense layers with
+ * dims[0..n_layers]; weights[l] is host [dims[l], dims[l+1]], biases[l] is
+ * host [1, dims[l+1]].  Hidden layers are ReLU and the output is linear, as
+ * in the reference plan (mod.rs:1418-1424).  batch fixes the plan's shapes. */
+int rt_mlp_create(rt_ctx* ctx, int n_layers, const size_t* dims, const float* const* weights,
+                  const float* const* biases, size_t batch, const rt_mlp_config* cfg, rt_mlp** out);
+int rt_mlp_destroy(rt_mlp* mlp);
+/* GpuMlp::step (mod.rs:1499-1511): forward, softmax cross-entropy, backward
+ * and optimizer update, enqueued without waiting.  x is [batch, dims[0]]
+ * (f32, or bf16 for RT_PREC_BF16), labels u32 [batch]. */
+int rt_mlp_step(rt_mlp* mlp, const rt_buf* x, const rt_buf* labels);
+/* GpuMlp::forward_only (mod.rs:1514-1521). */
+int rt_mlp_forward(rt_mlp* mlp, const rt_buf* x);
+/* GpuMlp::logits (mod.rs:1524-1526): blocking, n = batch*classes floats. */
+int rt_mlp_logits(rt_mlp* mlp, float* host, size_t n);
+/* GpuMlp::last_loss (mod.rs:1529-1531): blocking; mean of the per-row
+ * losses summed in row order.  Returns RT_ERR_LABEL if a label was >= C. */
+int rt_mlp_last_loss(rt_mlp* mlp, float* out);
+/* GpuMlp::weights / grads (mod.rs:1534-1551): blocking; host[i] receives
+ * parameter i of [W1, b1, W2, b2, ...] (f32; the master copy for bf16). */
+int rt_mlp_weights(rt_mlp* mlp, float* const* host, int n);
+int rt_mlp_grads(rt_mlp* mlp, float* const* host, int n);
+/* GpuMlp::dispatches_por_passo (mod.rs:1559-1561): kernel launches per step. */
+int rt_mlp_dispatches(rt_mlp* mlp, int* out);
+/* Whether the last completed step was skipped for a non-finite gradient
+ * under loss scaling (blocking). */
+int rt_mlp_overflow(rt_mlp* mlp, int* out);
+
+/* ------------------------------------------------------------- profiling */
+
+/* Gpu::perfilar (mod.rs:1245-1286): while enabled, every launch on ctx is
+ * bracketed by HIP events on the ctx stream.  rt_profile_report blocks and
+ * fills, per distinct kernel label, its name (up to name_len bytes), launch
+ * count and summed device milliseconds; returns the number of labels in
+ * *n_out (at most cap). */
+int rt_profile_enable(rt_ctx* ctx, int on);
+int rt_profile_reset(rt_ctx* ctx);
+int rt_profile_report(rt_ctx* ctx, char* names, size_t name_len, int* counts, double* ms, int cap,
+                      int* n_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RTENSOR_HIP_H */

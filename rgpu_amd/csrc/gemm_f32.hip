@@ -1,0 +1,393 @@
+// f32 GEMM on CDNA4 matrix cores: v_mfma_f32_16x16x4_f32, f32 accumulate.
+//
+// Replaces rtensor's MM_FAST / MM_EPILOGO / MM_SPLITK WGSL kernels
+// (crates/rtensor/src/gpu/gemm.rs:65-494, splitk.rs:33-237) for the three
+// operand layouts of the training step:
+//   NN  C = A·B      A [M,K] (K contiguous),  B [K,N] (N contiguous)  forward
+//   TN  C = Aᵀ·B     A [K,M] (M contiguous),  B [K,N] (N contiguous)  dW = Xᵀ·δ
+//   NT  C = A·Bᵀ     A [M,K] (K contiguous),  B [N,K] (K contiguous)  dX = δ·Wᵀ
+//
+// Block = 256 threads = 4 wave64s in a 2x2 arrangement; block tile BM x BN,
+// K staged through LDS 32 at a time, double-buffered with register staging
+// (one barrier per K step).  Each wave owns a (BM/2) x (BN/2) tile made of
+// TM x TN MFMA 16x16 tiles.
+//
+// Lane/element mapping.  A 16x16x4 MFMA takes, in lane l = 16g + r, the A
+// value (row r, k g) and the B value (k g, col r), and returns D(4g+q, r) in
+// accumulator register q.  Rows, columns and k inside a wave tile may be
+// permuted freely as long as A and B agree on k, so:
+//   * MFMA row r of row-tile t is wave row TM*r + t, MFMA col r of col-tile u
+//     is wave col TN*r + u: a lane's TM (TN) rows (cols) are adjacent, so one
+//     LDS vector read serves all of its tiles when the operand is M (N)
+//     contiguous, and the lane finally owns 4*TM adjacent rows x TN adjacent
+//     columns of C (vector stores along N);
+//   * within a 16-wide k chunk, MFMA step s of lane group g uses k = 4g + s,
+//     so a lane's 4 steps are adjacent k when the operand is K contiguous (one
+//     LDS vector read serves all four steps).
+//
+// Epilogues run on the accumulators in registers: bias, bias+ReLU (forward,
+// mm_bias in gemm.rs:452-493) and the ReLU mask (δ ← acc ⊙ 1[A>0], fusing
+// RELU_BWD, kernels.rs:119-131).  For TN with a colsum target the blocks of
+// the first M tile also sum the B tiles they stage in LDS over K: that is
+// db = 1ᵀ·δ (COLSUM, kernels.rs:182-199) at no extra HBM traffic.
+// With blockIdx.z > 0 splits, each slice writes a raw f32 partial plane and
+// splitk_reduce sums the planes in slice order (REDUZ, splitk.rs:240-256):
+// deterministic, no float atomics.
+
+#include "rt_internal.h"
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+constexpr int kThreads = 256;
+
+struct F32Args {
+  const float* A;
+  const float* B;
+  float* C;
+  int M, N, K, lda, ldb, ldc;
+  int epi;
+  const float* bias;
+  const float* mask;
+  float* colsum;  // [N], or [splits, N] partial rows when gridDim.z > 1
+  int k_per_split;
+  long long split_stride;
+  int tiles_m, tiles_n;
+  int vec_a, vec_b, vec_c;
+};
+
+// Loads `cnt` consecutive floats (cnt = 1, 2 or 4) from LDS as one access.
+template <int CNT>
+__device__ inline void lds_read(const float* p, float* out) {
+  if constexpr (CNT == 4) {
+    f4 v = *reinterpret_cast<const f4*>(p);
+    out[0] = v[0]; out[1] = v[1]; out[2] = v[2]; out[3] = v[3];
+  } else if constexpr (CNT == 2) {
+    f2 v = *reinterpret_cast<const f2*>(p);
+    out[0] = v[0]; out[1] = v[1];
+  } else {
+    out[0] = p[0];
+  }
+}
+
+// Global -> register load of one float4 of an operand tile.  `row`/`col`
+// index the stored matrix (row-major, leading dimension ld); the 4 elements
+// run along the contiguous dimension.  Out-of-range elements read as 0.
+__device__ inline f4 load4(const float* base, int ld, int row, int col, int rows, int cols, int vec) {
+  const float* src = base + (long long)row * ld + col;
+  if (vec && row < rows && col + 3 < cols) return *reinterpret_cast<const f4*>(src);
+  f4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = (row < rows && col + e < cols) ? src[e] : 0.0f;
+  return v;
+}
+
+template <int BM, int BN, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
+  constexpr int BK = 32, PAD = 4;
+  constexpr int TM = BM / 32, TN = BN / 32;  // MFMA tiles per wave (2x2 waves of BM/2 x BN/2)
+  constexpr int A_STRIDE = A_KC ? (BK + PAD) : (BM + PAD);
+  constexpr int B_STRIDE = B_KC ? (BK + PAD) : (BN + PAD);
+  constexpr int A_ELEMS = A_KC ? BM * A_STRIDE : BK * A_STRIDE;
+  constexpr int B_ELEMS = B_KC ? BN * B_STRIDE : BK * B_STRIDE;
+  constexpr int A_LD = BM / 32, B_LD = BN / 32;  // float4 loads per thread per K step
+  static_assert(BM % 32 == 0 && BN % 32 == 0 && BM <= 128 && BN <= 128, "tile");
+
+  __shared__ __attribute__((aligned(16))) float sA[2][A_ELEMS];
+  __shared__ __attribute__((aligned(16))) float sB[2][B_ELEMS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+
+  // Tile order.  Consecutive workgroups go to different XCDs (round robin
+  // over 8), each with its own L2: renumber so every XCD gets a contiguous
+  // run of tiles, then raster that run in groups of 8 M-tiles so the tiles
+  // resident on one XCD share A rows and B columns.
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * p.tiles_n;
+  const int grp = bid / per_group;
+  const int first_m = grp * GROUP;
+  const int gsize = min(p.tiles_m - first_m, GROUP);
+  const int in_grp = bid - grp * per_group;
+  const int tile_m = first_m + in_grp % gsize;
+  const int tile_n = in_grp / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const int kb = blockIdx.z * p.k_per_split;
+  const int ke = min(p.K, kb + p.k_per_split);
+  const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
+
+  f4 ra[A_LD], rb[B_LD];
+
+  auto load_tiles = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int idx = tid + kThreads * i;
+      if constexpr (A_KC) {
+        const int rr = idx >> 3, kq = idx & 7;  // 8 float4 per 32-wide K row
+        ra[i] = load4(p.A, p.lda, m0 + rr, k0 + 4 * kq, p.M, ke, p.vec_a);
+      } else {
+        constexpr int Q = BM / 4;
+        const int kk = idx / Q, mq = idx % Q;
+        ra[i] = load4(p.A, p.lda, k0 + kk, m0 + 4 * mq, ke, p.M, p.vec_a);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int idx = tid + kThreads * i;
+      if constexpr (B_KC) {
+        const int rr = idx >> 3, kq = idx & 7;
+        rb[i] = load4(p.B, p.ldb, n0 + rr, k0 + 4 * kq, p.N, ke, p.vec_b);
+      } else {
+        constexpr int Q = BN / 4;
+        const int kk = idx / Q, nq = idx % Q;
+        rb[i] = load4(p.B, p.ldb, k0 + kk, n0 + 4 * nq, ke, p.N, p.vec_b);
+      }
+    }
+  };
+  auto store_tiles = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int idx = tid + kThreads * i;
+      if constexpr (A_KC) {
+        *reinterpret_cast<f4*>(&sA[buf][(idx >> 3) * A_STRIDE + 4 * (idx & 7)]) = ra[i];
+      } else {
+        constexpr int Q = BM / 4;
+        *reinterpret_cast<f4*>(&sA[buf][(idx / Q) * A_STRIDE + 4 * (idx % Q)]) = ra[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int idx = tid + kThreads * i;
+      if constexpr (B_KC) {
+        *reinterpret_cast<f4*>(&sB[buf][(idx >> 3) * B_STRIDE + 4 * (idx & 7)]) = rb[i];
+      } else {
+        constexpr int Q = BN / 4;
+        *reinterpret_cast<f4*>(&sB[buf][(idx / Q) * B_STRIDE + 4 * (idx % Q)]) = rb[i];
+      }
+    }
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+#pragma unroll
+    for (int u = 0; u < TN; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](int buf) {
+    const float* as = sA[buf];
+    const float* bs = sB[buf];
+#pragma unroll
+    for (int ss = 0; ss < BK / 16; ++ss) {
+      float af[TM][4], bf[TN][4];
+      if constexpr (A_KC) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) lds_read<4>(&as[(wm + TM * r + t) * A_STRIDE + ss * 16 + 4 * g], af[t]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float tmp[TM];
+          lds_read<TM>(&as[(ss * 16 + 4 * g + s) * A_STRIDE + wm + TM * r], tmp);
+#pragma unroll
+          for (int t = 0; t < TM; ++t) af[t][s] = tmp[t];
+        }
+      }
+      if constexpr (B_KC) {
+#pragma unroll
+        for (int u = 0; u < TN; ++u) lds_read<4>(&bs[(wn + TN * r + u) * B_STRIDE + ss * 16 + 4 * g], bf[u]);
+      } else {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          float tmp[TN];
+          lds_read<TN>(&bs[(ss * 16 + 4 * g + s) * B_STRIDE + wn + TN * r], tmp);
+#pragma unroll
+          for (int u = 0; u < TN; ++u) bf[u][s] = tmp[u];
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < TM; ++t)
+#pragma unroll
+          for (int u = 0; u < TN; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t][s], bf[u][s], acc[t][u], 0, 0, 0);
+    }
+  };
+
+  // Column sums of B (the bias gradient when B = δ), from the LDS tiles of
+  // the first M tile's blocks, summed over k in increasing order.
+  const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0 && tid < BN;
+  float cs = 0.0f;
+
+  if (nk > 0) {
+    load_tiles(kb);
+    store_tiles(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load_tiles(kb + (kt + 1) * BK);
+      compute(cur);
+      if constexpr (!B_KC) {
+        if (do_cs) {
+          const float* bs = sB[cur];
+#pragma unroll 8
+          for (int kk = 0; kk < BK; ++kk) cs += bs[kk * B_STRIDE + tid];
+        }
+      }
+      if (kt + 1 < nk) store_tiles(cur ^ 1);
+      __syncthreads();
+    }
+  }
+
+  if (do_cs && n0 + tid < p.N) p.colsum[(long long)blockIdx.z * p.N + n0 + tid] = cs;
+
+  // Epilogue.  Lane owns rows m0+wm+TM*(4g+q)+t and columns n0+wn+TN*r+u.
+  const bool partial = gridDim.z > 1;
+  float* Cout = p.C + (long long)blockIdx.z * p.split_stride;
+  const int col0 = n0 + wn + TN * r;
+  float bias_v[TN];
+#pragma unroll
+  for (int u = 0; u < TN; ++u)
+    bias_v[u] = (!partial && p.bias != nullptr && col0 + u < p.N) ? p.bias[col0 + u] : 0.0f;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+      const int row = m0 + wm + TM * (4 * g + q) + t;
+      if (row >= p.M) continue;
+      float v[TN];
+#pragma unroll
+      for (int u = 0; u < TN; ++u) v[u] = acc[t][u][q];
+      if (!partial) {
+        if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
+#pragma unroll
+          for (int u = 0; u < TN; ++u) v[u] = v[u] + bias_v[u];
+          if (p.epi == RT_EPI_BIAS_RELU) {
+#pragma unroll
+            for (int u = 0; u < TN; ++u) v[u] = fmaxf(v[u], 0.0f);
+          }
+        } else if (p.epi == RT_EPI_RELU_MASK) {
+          const float* mrow = p.mask + (long long)row * p.ldc;
+#pragma unroll
+          for (int u = 0; u < TN; ++u)
+            if (col0 + u < p.N && !(mrow[col0 + u] > 0.0f)) v[u] = 0.0f;
+        }
+      }
+      float* dst = Cout + (long long)row * p.ldc + col0;
+      if constexpr (TN == 4) {
+        if (p.vec_c && col0 + 3 < p.N) {
+          *reinterpret_cast<f4*>(dst) = f4{v[0], v[1], v[2], v[3]};
+          continue;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < TN; ++u)
+        if (col0 + u < p.N) dst[u] = v[u];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, long long stride,
+                                                             int M, int N, float* C, int ldc, int epi,
+                                                             const float* bias, const float* mask,
+                                                             const float* cs_part, float* cs) {
+  const long long total = (long long)M * N;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    float v = part[i];
+    for (int s = 1; s < S; ++s) v += part[s * stride + i];
+    const int row = (int)(i / N), col = (int)(i % N);
+    if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) {
+      v = v + bias[col];
+      if (epi == RT_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
+    } else if (epi == RT_EPI_RELU_MASK) {
+      if (!(mask[(long long)row * ldc + col] > 0.0f)) v = 0.0f;
+    }
+    C[(long long)row * ldc + col] = v;
+  }
+  if (cs != nullptr) {
+    for (long long j = blockIdx.x * (long long)blockDim.x + threadIdx.x; j < N; j += (long long)gridDim.x * blockDim.x) {
+      float v = cs_part[j];
+      for (int s = 1; s < S; ++s) v += cs_part[(long long)s * N + j];
+      cs[j] = v;
+    }
+  }
+}
+
+template <int BM, int BN, bool A_KC, bool B_KC>
+hipError_t launch_f32(hipStream_t s, F32Args a, int splits) {
+  a.tiles_m = (a.M + BM - 1) / BM;
+  a.tiles_n = (a.N + BN - 1) / BN;
+  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_KC, B_KC>), grid, dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+template <bool A_KC, bool B_KC>
+hipError_t dispatch_tile(hipStream_t s, F32Args a, int splits) {
+  // 128x128 tiles when they alone give at least two waves of 256 CUs,
+  // otherwise 64x64 (4x the workgroups) so small GEMMs still fill the chip.
+  const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
+  if (t128 >= 512) return launch_f32<128, 128, A_KC, B_KC>(s, a, splits);
+  if (a.N <= 32) return launch_f32<64, 32, A_KC, B_KC>(s, a, splits);
+  return launch_f32<64, 64, A_KC, B_KC>(s, a, splits);
+}
+
+}  // namespace
+
+namespace rt {
+
+hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d) {
+  F32Args a{};
+  a.A = static_cast<const float*>(d.A);
+  a.B = static_cast<const float*>(d.B);
+  a.C = static_cast<float*>(d.C);
+  a.M = d.M;
+  a.N = d.N;
+  a.K = d.K;
+  a.lda = d.lda;
+  a.ldb = d.ldb;
+  a.ldc = d.ldc;
+  a.epi = d.epi;
+  a.bias = d.bias;
+  a.mask = static_cast<const float*>(d.mask);
+  a.colsum = d.splits > 1 ? d.colsum_partials : d.colsum;
+  const int splits = d.splits < 1 ? 1 : d.splits;
+  // Slices are whole multiples of the 32-wide K step.
+  int kps = (d.K + splits - 1) / splits;
+  kps = ((kps + 31) / 32) * 32;
+  a.k_per_split = splits > 1 ? kps : (d.K > 0 ? d.K : 1);
+  a.split_stride = d.split_stride;
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  a.vec_a = (d.lda % 4 == 0) && al16(d.A);
+  a.vec_b = (d.ldb % 4 == 0) && al16(d.B);
+  a.vec_c = (d.ldc % 4 == 0) && al16(d.C);
+  switch (d.layout) {
+    case RT_NN: return dispatch_tile<true, false>(s, a, splits);
+    case RT_TN: return dispatch_tile<false, false>(s, a, splits);
+    case RT_NT: return dispatch_tile<true, true>(s, a, splits);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M, int N,
+                                void* C, int out_dtype, int ldc, int epi, const float* bias, const void* mask,
+                                int mask_dtype, const float* colsum_partials, float* colsum) {
+  if (out_dtype != RT_F32 || mask_dtype != RT_F32) return hipErrorInvalidValue;
+  const long long total = (long long)M * N;
+  int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partials, splits, stride, M, N,
+                     static_cast<float*>(C), ldc, epi, bias, static_cast<const float*>(mask), colsum_partials,
+                     colsum);
+  return hipGetLastError();
+}
+
+}  // namespace rt

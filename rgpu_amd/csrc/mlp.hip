@@ -1,0 +1,460 @@
+// The MLP training plan: rtensor's GpuMlp (crates/rtensor/src/gpu/mod.rs:1291-1562)
+// rebuilt around one HIP stream and one device arena.
+//
+// Memory layout (one hipMalloc, every region 256-byte aligned):
+//   theta | grad | m | v     flat f32 vectors in parameter order
+//                            [W1, b1, W2, b2, ...], each segment padded to a
+//                            multiple of 64 floats, so the whole optimizer is
+//                            one contiguous sweep (padding stays zero)
+//   theta_bf16               bf16 copy of theta written by the optimizer
+//                            (mixed precision only)
+//   act[l], delta[l]         [batch, dims[l+1]] per layer: post-ReLU
+//                            activation of hidden layers (the ReLU mask comes
+//                            from it, as mod.rs:1453-1455 notes), logits for
+//                            the last layer; δ = ∂L/∂Z
+//   partials                 split-K planes (largest user), reused by every
+//                            split GEMM of the step
+//   loss_rows [batch]
+//
+// Step (mod.rs:1399-1467 order): forward GEMMs with bias(+ReLU) epilogues;
+// softmax-xent → δ_L; per layer, last to first: dW = A_{l-1}ᵀ·δ_l with the
+// bias gradient summed from the same δ tiles, then (l > 0)
+// δ_{l-1} = (δ_l·W_lᵀ) ⊙ 1[A_{l-1} > 0]; then one fused optimizer launch.
+// Narrow layers (the 10-class head, its dW) use split-K with a fixed-order
+// reduction, chosen by rt_splitk_slices.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "rt_internal.h"
+
+namespace rt {
+hipError_t gemm_launch(hipStream_t s, const GemmDesc& d);
+}
+using namespace rt;
+
+namespace {
+
+struct Layer {
+  size_t din = 0, dout = 0;
+  size_t w_off = 0, b_off = 0;  // offsets (floats) into the flat parameter vectors
+  void* act = nullptr;          // [batch, dout], f32 (or bf16 for mixed-precision hidden layers)
+  float* delta = nullptr;       // [batch, dout] f32
+  void* delta_h = nullptr;      // [batch, dout] bf16 (mixed precision)
+  int splits_dw = 1;
+  int splits_fwd = 1;
+  std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx;
+};
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+struct rt_mlp {
+  rt_ctx* ctx = nullptr;
+  size_t batch = 0;
+  int n_layers = 0;
+  rt_mlp_config cfg{};
+  std::vector<Layer> L;
+  size_t n_params = 0;  // padded flat length
+  char* arena = nullptr;
+  float* theta = nullptr;
+  float* grad = nullptr;
+  float* m = nullptr;
+  float* v = nullptr;
+  void* theta_h = nullptr;  // bf16 copy
+  float* partials = nullptr;
+  size_t partial_elems = 0;
+  float* loss_rows = nullptr;
+  int t = 0;
+  int dispatches = 0;
+  bool mixed = false;
+  const rt_buf* last_x = nullptr;
+};
+
+static bool valid_cfg(const rt_mlp_config* c) {
+  if (c->optimizer != RT_OPT_ADAM && c->optimizer != RT_OPT_SGD) return false;
+  if (c->precision != RT_PREC_F32 && c->precision != RT_PREC_BF16) return false;
+  if (!(c->loss_scale > 0.0f) || !std::isfinite(c->loss_scale)) return false;
+  return true;
+}
+
+// Run one GEMM of the plan, with optional split-K.
+static int plan_gemm(rt_mlp* p, const char* lbl, const char* lbl_red, int layout, int in_dtype, const void* A,
+                     const void* B, void* C, int out_dtype, int M, int N, int K, int lda, int ldb, int epi,
+                     const float* bias, const void* mask, int mask_dtype, float* colsum, int splits) {
+  rt_ctx* c = p->ctx;
+  GemmDesc d;
+  d.layout = layout;
+  d.in_dtype = in_dtype;
+  d.out_dtype = out_dtype;
+  d.A = A;
+  d.B = B;
+  d.M = M;
+  d.N = N;
+  d.K = K;
+  d.lda = lda;
+  d.ldb = ldb;
+  d.ldc = N;
+  if (splits <= 1) {
+    d.C = C;
+    d.epi = epi;
+    d.bias = bias;
+    d.mask = mask;
+    d.mask_dtype = mask_dtype;
+    d.colsum = colsum;
+    Launch Lz(c, lbl);
+    hipError_t e = gemm_launch(c->stream, d);
+    if (e != hipSuccess) return hip_fail(c, e, lbl);
+    return RT_OK;
+  }
+  d.C = p->partials;
+  d.out_dtype = RT_F32;
+  d.splits = splits;
+  d.split_stride = (long long)M * N;
+  d.colsum_partials = colsum ? p->partials + (size_t)splits * M * N : nullptr;
+  {
+    Launch Lz(c, lbl);
+    hipError_t e = gemm_launch(c->stream, d);
+    if (e != hipSuccess) return hip_fail(c, e, lbl);
+  }
+  Launch Lz(c, lbl_red);
+  hipError_t e = splitk_reduce_launch(c->stream, p->partials, splits, (long long)M * N, M, N, C, out_dtype, N, epi,
+                                      bias, mask, mask_dtype, d.colsum_partials, colsum);
+  if (e != hipSuccess) return hip_fail(c, e, lbl_red);
+  return RT_OK;
+}
+
+static int run_forward(rt_mlp* p, const rt_buf* x) {
+  const int nl = p->n_layers;
+  const int B = (int)p->batch;
+  const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
+  for (int l = 0; l < nl; ++l) {
+    Layer& Ly = p->L[l];
+    const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
+    const bool last = l == nl - 1;
+    const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
+    const float* bias = p->theta + Ly.b_off;
+    const int out_dtype = (p->mixed && !last) ? RT_BF16 : RT_F32;
+    int rc = plan_gemm(p, Ly.lbl_fwd.c_str(), Ly.lbl_fwd_red.c_str(), RT_NN, in_dtype, in, W, Ly.act, out_dtype, B,
+                       (int)Ly.dout, (int)Ly.din, (int)Ly.din, (int)Ly.dout, last ? RT_EPI_BIAS : RT_EPI_BIAS_RELU,
+                       bias, nullptr, RT_F32, nullptr, Ly.splits_fwd);
+    if (rc) return rc;
+  }
+  return RT_OK;
+}
+
+extern "C" {
+
+int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* const* weights, const float* const* biases,
+                  size_t batch, const rt_mlp_config* cfg, rt_mlp** out) {
+  if (c == nullptr) return RT_ERR_INVALID;
+  if (out == nullptr || dims == nullptr || weights == nullptr || biases == nullptr || cfg == nullptr)
+    return fail(c, RT_ERR_INVALID, "null argument");
+  *out = nullptr;
+  if (n_layers < 1 || n_layers > kMaxOptTensors / 2) return fail(c, RT_ERR_INVALID, "n_layers must be in [1, 12]");
+  if (batch < 1 || batch > (1u << 30)) return fail(c, RT_ERR_INVALID, "batch must be >= 1");
+  if (!valid_cfg(cfg)) return fail(c, RT_ERR_INVALID, "bad rt_mlp_config");
+  for (int l = 0; l <= n_layers; ++l)
+    if (dims[l] < 1 || dims[l] > (1u << 24)) return fail(c, RT_ERR_SHAPE, "layer width %d out of range", l);
+  for (int l = 0; l < n_layers; ++l)
+    if (!weights[l] || !biases[l]) return fail(c, RT_ERR_INVALID, "null parameter %d", l);
+
+  auto* p = new rt_mlp();
+  p->ctx = c;
+  p->batch = batch;
+  p->n_layers = n_layers;
+  p->cfg = *cfg;
+  p->mixed = cfg->precision == RT_PREC_BF16;
+  p->L.resize(n_layers);
+
+  size_t off = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    Layer& Ly = p->L[l];
+    Ly.din = dims[l];
+    Ly.dout = dims[l + 1];
+    Ly.w_off = off;
+    off += round_up(Ly.din * Ly.dout, 64);
+    Ly.b_off = off;
+    off += round_up(Ly.dout, 64);
+    const bool last = l == n_layers - 1;
+    // Forward split-K only on the linear output layer (mod.rs:1360-1367):
+    // hidden layers are wide enough, and the ReLU epilogue stays fused.
+    Ly.splits_fwd = last ? (int)rt_splitk_slices(batch, Ly.dout, Ly.din) : 1;
+    Ly.splits_dw = (int)rt_splitk_slices(Ly.din, Ly.dout, batch);
+    Ly.lbl_fwd = "fwd_l" + std::to_string(l);
+    Ly.lbl_fwd_red = "fwd_reduce_l" + std::to_string(l);
+    Ly.lbl_dw = "dw_l" + std::to_string(l);
+    Ly.lbl_dw_red = "dw_reduce_l" + std::to_string(l);
+    Ly.lbl_dx = "dx_l" + std::to_string(l);
+  }
+  p->n_params = off;
+
+  size_t part = 0;
+  for (auto& Ly : p->L) {
+    if (Ly.splits_fwd > 1) part = std::max(part, (size_t)Ly.splits_fwd * batch * Ly.dout);
+    if (Ly.splits_dw > 1) part = std::max(part, (size_t)Ly.splits_dw * (Ly.din * Ly.dout + Ly.dout));
+  }
+  p->partial_elems = part;
+
+  // Arena layout.
+  const size_t A = 256;
+  size_t bytes = 0;
+  auto reserve = [&](size_t nbytes) {
+    size_t o = bytes;
+    bytes += round_up(std::max<size_t>(nbytes, 1), A);
+    return o;
+  };
+  size_t o_theta = reserve(p->n_params * 4), o_grad = reserve(p->n_params * 4), o_m = reserve(p->n_params * 4),
+         o_v = reserve(p->n_params * 4);
+  size_t o_theta_h = p->mixed ? reserve(p->n_params * 2) : 0;
+  std::vector<size_t> o_act(n_layers), o_delta(n_layers), o_delta_h(n_layers);
+  for (int l = 0; l < n_layers; ++l) {
+    const bool last = l == n_layers - 1;
+    size_t elems = batch * p->L[l].dout;
+    o_act[l] = reserve(elems * ((p->mixed && !last) ? 2 : 4));
+    o_delta[l] = reserve(elems * 4);
+    o_delta_h[l] = p->mixed ? reserve(elems * 2) : 0;
+  }
+  size_t o_part = reserve(part * 4);
+  size_t o_loss = reserve(batch * 4);
+
+  hipError_t e = hipSetDevice(c->device);
+  if (e == hipSuccess) e = hipMalloc(&p->arena, bytes);
+  if (e != hipSuccess) {
+    delete p;
+    return hip_fail(c, e, "mlp arena");
+  }
+  p->theta = (float*)(p->arena + o_theta);
+  p->grad = (float*)(p->arena + o_grad);
+  p->m = (float*)(p->arena + o_m);
+  p->v = (float*)(p->arena + o_v);
+  p->theta_h = p->mixed ? (void*)(p->arena + o_theta_h) : nullptr;
+  for (int l = 0; l < n_layers; ++l) {
+    p->L[l].act = p->arena + o_act[l];
+    p->L[l].delta = (float*)(p->arena + o_delta[l]);
+    p->L[l].delta_h = p->mixed ? (void*)(p->arena + o_delta_h[l]) : nullptr;
+  }
+  p->partials = part ? (float*)(p->arena + o_part) : nullptr;
+  p->loss_rows = (float*)(p->arena + o_loss);
+
+  // Zero everything (padding and moments must start at 0), then upload θ.
+  e = fill_i32_launch(c->stream, (int*)p->arena, 0, bytes / 4);
+  std::vector<float> host(p->n_params, 0.0f);
+  for (int l = 0; l < n_layers && e == hipSuccess; ++l) {
+    const Layer& Ly = p->L[l];
+    std::memcpy(&host[Ly.w_off], weights[l], Ly.din * Ly.dout * 4);
+    std::memcpy(&host[Ly.b_off], biases[l], Ly.dout * 4);
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(p->theta, host.data(), p->n_params * 4, hipMemcpyHostToDevice, c->stream);
+  if (e == hipSuccess && p->mixed) e = convert_launch(c->stream, p->theta, RT_F32, p->theta_h, RT_BF16, p->n_params);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    hipFree(p->arena);
+    delete p;
+    return hip_fail(c, e, "mlp init");
+  }
+
+  // Launch count of one step.
+  int n = 0;
+  for (int l = 0; l < n_layers; ++l) {
+    n += p->L[l].splits_fwd > 1 ? 2 : 1;
+    n += p->L[l].splits_dw > 1 ? 2 : 1;
+    if (l > 0) n += 1;
+  }
+  n += 1;  // softmax-xent
+  n += 1;  // optimizer
+  if (p->mixed) n += 2;  // overflow flag reset + non-finite check
+  p->dispatches = n;
+  *out = p;
+  return RT_OK;
+}
+
+int rt_mlp_destroy(rt_mlp* p) {
+  if (p == nullptr) return RT_OK;
+  hipStreamSynchronize(p->ctx->stream);
+  hipFree(p->arena);
+  delete p;
+  return RT_OK;
+}
+
+static int check_inputs(rt_mlp* p, const rt_buf* x) {
+  rt_ctx* c = p->ctx;
+  if (x == nullptr) return fail(c, RT_ERR_INVALID, "null batch");
+  const rt_dtype want = p->mixed ? RT_BF16 : RT_F32;
+  if (x->dtype != want) return fail(c, RT_ERR_DTYPE, "batch must be %s", p->mixed ? "bf16" : "f32");
+  if (x->n != p->batch * p->L[0].din)
+    return fail(c, RT_ERR_SHAPE, "batch with %zu elements, plan built for %zu", x->n, p->batch * p->L[0].din);
+  return RT_OK;
+}
+
+int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  int rc = check_inputs(p, x);
+  if (rc) return rc;
+  if (labels == nullptr || labels->dtype != RT_U32 || labels->n != p->batch)
+    return fail(c, RT_ERR_SHAPE, "labels must be u32 [%zu]", p->batch);
+  const int nl = p->n_layers;
+  const int B = (int)p->batch;
+  const float scale = p->mixed ? p->cfg.loss_scale : 1.0f;
+  int* overflow = c->d_flags + 1;
+
+  if (p->mixed) {
+    Launch Lz(c, "overflow_reset");
+    hipError_t e = fill_i32_launch(c->stream, overflow, 0, 1);
+    if (e != hipSuccess) return hip_fail(c, e, "overflow reset");
+  }
+  if ((rc = run_forward(p, x))) return rc;
+
+  Layer& top = p->L[nl - 1];
+  {
+    Launch Lz(c, "softmax_xent");
+    hipError_t e = xent_launch(c->stream, (const float*)top.act, (const uint32_t*)labels->ptr, top.delta, top.delta_h,
+                               p->loss_rows, B, (int)top.dout, scale / (float)B, c->d_flags);
+    if (e != hipSuccess) return hip_fail(c, e, "softmax_xent");
+  }
+
+  const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
+  for (int l = nl - 1; l >= 0; --l) {
+    Layer& Ly = p->L[l];
+    const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
+    const void* dl = p->mixed ? Ly.delta_h : (const void*)Ly.delta;
+    // dW_l = A_{l-1}ᵀ·δ_l  (TN; A stored [batch, din]), db_l = 1ᵀ·δ_l fused.
+    rc = plan_gemm(p, Ly.lbl_dw.c_str(), Ly.lbl_dw_red.c_str(), RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32,
+                   (int)Ly.din, (int)Ly.dout, B, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32,
+                   p->grad + Ly.b_off, Ly.splits_dw);
+    if (rc) return rc;
+    if (l > 0) {
+      Layer& Lp = p->L[l - 1];
+      const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
+      // δ_{l-1} = (δ_l·W_lᵀ) ⊙ 1[A_{l-1} > 0]  (NT; W stored [din, dout] = [N, K]).
+      void* dst = p->mixed ? Lp.delta_h : (void*)Lp.delta;
+      rc = plan_gemm(p, Ly.lbl_dx.c_str(), "", RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B,
+                     (int)Ly.din, (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
+                     p->mixed ? RT_BF16 : RT_F32, nullptr, 1);
+      if (rc) return rc;
+    }
+  }
+
+  if (p->mixed) {
+    const float* ptrs[1] = {p->grad};
+    size_t ns[1] = {p->n_params};
+    Launch Lz(c, "nonfinite_check");
+    hipError_t e = nonfinite_check_launch(c->stream, ptrs, ns, 1, overflow);
+    if (e != hipSuccess) return hip_fail(c, e, "non-finite check");
+  }
+
+  p->t += 1;
+  OptTensor T{p->theta, p->grad, p->m, p->v, p->theta_h, p->n_params};
+  OptParams P;
+  P.kind = p->cfg.optimizer == RT_OPT_ADAM ? 0 : 1;
+  P.lr = p->cfg.lr;
+  P.beta1 = p->cfg.beta1;
+  P.beta2 = p->cfg.beta2;
+  P.eps = p->cfg.eps;
+  P.momentum = p->cfg.momentum;
+  if (P.kind == 0) {
+    const float c1 = 1.0f - powi_f32(P.beta1, p->t), c2 = 1.0f - powi_f32(P.beta2, p->t);
+    P.inv_c1 = 1.0f / c1;
+    P.inv_c2 = 1.0f / c2;
+  }
+  if (p->mixed) {
+    P.grad_scale = 1.0f / p->cfg.loss_scale;
+    P.skip_flag = overflow;
+  }
+  if (P.kind == 1 && P.momentum == 0.0f) T.m = nullptr;
+  Launch Lz(c, "optimizer");
+  hipError_t e = optimizer_launch(c->stream, &T, 1, P);
+  if (e != hipSuccess) return hip_fail(c, e, "optimizer");
+  return RT_OK;
+}
+
+int rt_mlp_forward(rt_mlp* p, const rt_buf* x) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  int rc = check_inputs(p, x);
+  if (rc) return rc;
+  return run_forward(p, x);
+}
+
+int rt_mlp_logits(rt_mlp* p, float* host, size_t n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  const Layer& top = p->L[p->n_layers - 1];
+  if (host == nullptr || n != p->batch * top.dout) return fail(c, RT_ERR_SHAPE, "logits need %zu floats", p->batch * top.dout);
+  hipError_t e = hipMemcpyAsync(host, top.act, n * 4, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "logits");
+  return RT_OK;
+}
+
+int rt_mlp_last_loss(rt_mlp* p, float* out) {
+  if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  std::vector<float> rows(p->batch);
+  int flag = 0;
+  hipError_t e = hipMemcpyAsync(rows.data(), p->loss_rows, p->batch * 4, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipMemcpyAsync(&flag, c->d_flags, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "last_loss");
+  if (flag != 0) {
+    // Sticky until reported: clear it so later steps start clean.
+    e = fill_i32_launch(c->stream, c->d_flags, 0, 1);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "flag reset");
+    return fail(c, RT_ERR_LABEL, "a label was >= the number of classes (%zu)", p->L[p->n_layers - 1].dout);
+  }
+  // Tensor::mean_all (tensor.rs:284-286): sequential f32 sum, then divide.
+  float s = 0.0f;
+  for (float r : rows) s += r;
+  *out = s / (float)p->batch;
+  return RT_OK;
+}
+
+static int fetch(rt_mlp* p, const float* base, float* const* host, int n) {
+  rt_ctx* c = p->ctx;
+  if (host == nullptr || n != 2 * p->n_layers) return fail(c, RT_ERR_SHAPE, "need %d host arrays", 2 * p->n_layers);
+  for (int i = 0; i < n; ++i)
+    if (host[i] == nullptr) return fail(c, RT_ERR_INVALID, "null host array %d", i);
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < p->n_layers && e == hipSuccess; ++l) {
+    const Layer& Ly = p->L[l];
+    e = hipMemcpyAsync(host[2 * l], base + Ly.w_off, Ly.din * Ly.dout * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(host[2 * l + 1], base + Ly.b_off, Ly.dout * 4, hipMemcpyDeviceToHost, c->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "download parameters");
+  return RT_OK;
+}
+
+int rt_mlp_weights(rt_mlp* p, float* const* host, int n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  return fetch(p, p->theta, host, n);
+}
+
+int rt_mlp_grads(rt_mlp* p, float* const* host, int n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  return fetch(p, p->grad, host, n);
+}
+
+int rt_mlp_dispatches(rt_mlp* p, int* out) {
+  if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
+  *out = p->dispatches;
+  return RT_OK;
+}
+
+int rt_mlp_overflow(rt_mlp* p, int* out) {
+  if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  int flag = 0;
+  hipError_t e = hipMemcpyAsync(&flag, c->d_flags + 1, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "overflow flag");
+  *out = flag;
+  return RT_OK;
+}
+
+}  // extern "C"

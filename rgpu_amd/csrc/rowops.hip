@@ -1,0 +1,227 @@
+// Row and column kernels of the training step (all HBM- or latency-bound):
+//   softmax cross-entropy   XENT      kernels.rs:138-167  (one wave64 per row)
+//   column sum              COLSUM    kernels.rs:182-199  (two fixed-order stages)
+//   bias add / ReLU / ReLU backward   kernels.rs:99-131
+//   f32 <-> bf16/f16 conversion       EMPACOTA mista.rs:326-341
+// Built with -ffp-contract=off: every product and sum rounds on its own, in
+// the order rtensor's CPU path uses (losses.rs:99-115, tensor.rs:455-472).
+
+#include <algorithm>
+
+#include "rt_internal.h"
+
+namespace {
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ inline unsigned short f32_to_bf16_rne(float x) {
+  unsigned int u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (unsigned short)(u >> 16);
+}
+
+__device__ inline float bf16_to_f32(unsigned short h) { return __uint_as_float((unsigned int)h << 16); }
+
+// One wave per row: max, Σexp, p = e/Σ, δ = (p − onehot)·scale, loss = −ln max(p_y, 1e-12).
+// A label >= cols raises err_flag (plain store) and makes that row's loss NaN;
+// nothing is read out of bounds.
+__global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ logits, const uint32_t* __restrict__ labels,
+                                                   float* __restrict__ delta, unsigned short* __restrict__ delta_bf16,
+                                                   float* __restrict__ loss_rows, int rows, int cols, float scale,
+                                                   int* err_flag) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* z = logits + (long long)row * cols;
+  float mx = -INFINITY;
+  for (int j = lane; j < cols; j += 64) mx = fmaxf(mx, z[j]);
+  mx = wave_max(mx);
+  float sum = 0.0f;
+  for (int j = lane; j < cols; j += 64) sum += expf(z[j] - mx);
+  sum = wave_sum(sum);
+  const uint32_t y = labels[row];
+  const bool bad = y >= (uint32_t)cols;
+  if (bad && lane == 0) {
+    *err_flag = 1;
+    loss_rows[row] = __uint_as_float(0x7fc00000u);
+  }
+  float* d = delta + (long long)row * cols;
+  for (int j = lane; j < cols; j += 64) {
+    const float pj = expf(z[j] - mx) / sum;
+    const float yj = (!bad && (uint32_t)j == y) ? 1.0f : 0.0f;
+    const float dj = (pj - yj) * scale;
+    d[j] = dj;
+    if (delta_bf16 != nullptr) delta_bf16[(long long)row * cols + j] = f32_to_bf16_rne(dj);
+    if (!bad && (uint32_t)j == y) loss_rows[row] = -logf(fmaxf(pj, 1e-12f));
+  }
+}
+
+// Stage 1: block (cx, cy) sums rows [cy*chunk, (cy+1)*chunk) of 256 columns
+// starting at cx*256, one column per thread, rows in increasing order.
+template <typename T>
+__device__ inline float load_as_f32(const T* p, long long i);
+template <>
+__device__ inline float load_as_f32<float>(const float* p, long long i) { return p[i]; }
+template <>
+__device__ inline float load_as_f32<unsigned short>(const unsigned short* p, long long i) { return bf16_to_f32(p[i]); }
+template <>
+__device__ inline float load_as_f32<_Float16>(const _Float16* p, long long i) { return (float)p[i]; }
+
+template <typename T>
+__global__ __launch_bounds__(256) void colsum_stage1(const T* __restrict__ src, int rows, int cols, int chunk,
+                                                     float* __restrict__ out) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  const int r0 = blockIdx.y * chunk;
+  const int r1 = min(rows, r0 + chunk);
+  float acc = 0.0f;
+  for (int r = r0; r < r1; ++r) acc += load_as_f32<T>(src, (long long)r * cols + c);
+  out[(long long)blockIdx.y * cols + c] = acc;
+}
+
+__global__ __launch_bounds__(256) void colsum_stage2(const float* __restrict__ part, int parts, int cols,
+                                                     float* __restrict__ dst) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  float acc = 0.0f;
+  for (int s = 0; s < parts; ++s) acc += part[(long long)s * cols + c];
+  dst[c] = acc;
+}
+
+__global__ __launch_bounds__(256) void bias_add_kernel(float* z, const float* b, int rows, int cols) {
+  const long long total = (long long)rows * cols;
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < total; i += (long long)gridDim.x * 256)
+    z[i] = z[i] + b[i % cols];
+}
+
+__global__ __launch_bounds__(256) void relu_kernel(const float* x, float* y, long long n) {
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (long long)gridDim.x * 256) y[i] = fmaxf(x[i], 0.0f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void relu_bwd_kernel(const T* a, float* delta, long long n) {
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (long long)gridDim.x * 256)
+    if (!(load_as_f32<T>(a, i) > 0.0f)) delta[i] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void convert_kernel(const void* src, int sd, void* dst, int dd, long long n) {
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (long long)gridDim.x * 256) {
+    float v;
+    if (sd == RT_F32) v = static_cast<const float*>(src)[i];
+    else if (sd == RT_BF16) v = bf16_to_f32(static_cast<const unsigned short*>(src)[i]);
+    else v = (float)static_cast<const _Float16*>(src)[i];
+    if (dd == RT_F32) static_cast<float*>(dst)[i] = v;
+    else if (dd == RT_BF16) static_cast<unsigned short*>(dst)[i] = f32_to_bf16_rne(v);
+    else static_cast<_Float16*>(dst)[i] = (_Float16)v;  // v_cvt_f16_f32: round to nearest even, keeps subnormals
+  }
+}
+
+__global__ void fill_i32_kernel(int* p, int v, long long n) {
+  for (long long i = blockIdx.x * 256LL + threadIdx.x; i < n; i += (long long)gridDim.x * 256) p[i] = v;
+}
+
+int grid_for(long long n) {
+  long long b = (n + 255) / 256;
+  return (int)std::max<long long>(1, std::min<long long>(b, 8192));
+}
+
+}  // namespace
+
+namespace rt {
+
+hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* labels, float* delta, void* delta_half,
+                       float* loss_rows, int rows, int cols, float scale, int* err_flag) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(xent_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, logits, labels, delta,
+                     static_cast<unsigned short*>(delta_half), loss_rows, rows, cols, scale, err_flag);
+  return hipGetLastError();
+}
+
+// Rows per stage-1 chunk: enough chunks that the column blocks times chunks
+// give ~2048 workgroups, but at least 8 rows each.
+static int colsum_chunk(int rows, int cols) {
+  const int cblocks = (cols + 255) / 256;
+  int want = std::max(1, 2048 / cblocks);
+  int chunk = (rows + want - 1) / want;
+  return std::max(chunk, 8);
+}
+
+size_t colsum_scratch_elems(int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  const int chunk = colsum_chunk(rows, cols);
+  const int parts = (rows + chunk - 1) / chunk;
+  return parts > 1 ? (size_t)parts * cols : 0;
+}
+
+hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, int cols, float* dst, float* scratch,
+                         size_t scratch_elems) {
+  if (cols <= 0) return hipSuccess;
+  if (rows <= 0) {
+    hipLaunchKernelGGL(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, (const float*)nullptr, 0, cols, dst);
+    return hipGetLastError();
+  }
+  const int chunk = colsum_chunk(rows, cols);
+  const int parts = (rows + chunk - 1) / chunk;
+  float* out1 = parts > 1 ? scratch : dst;
+  if (parts > 1 && (scratch == nullptr || scratch_elems < (size_t)parts * cols)) return hipErrorInvalidValue;
+  dim3 g1((cols + 255) / 256, parts);
+  if (dtype == RT_F32)
+    hipLaunchKernelGGL(colsum_stage1<float>, g1, dim3(256), 0, s, static_cast<const float*>(src), rows, cols, chunk, out1);
+  else if (dtype == RT_BF16)
+    hipLaunchKernelGGL(colsum_stage1<unsigned short>, g1, dim3(256), 0, s, static_cast<const unsigned short*>(src),
+                       rows, cols, chunk, out1);
+  else
+    hipLaunchKernelGGL(colsum_stage1<_Float16>, g1, dim3(256), 0, s, static_cast<const _Float16*>(src), rows, cols,
+                       chunk, out1);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || parts == 1) return e;
+  hipLaunchKernelGGL(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, scratch, parts, cols, dst);
+  return hipGetLastError();
+}
+
+hipError_t bias_add_launch(hipStream_t s, float* z, const float* b, int rows, int cols) {
+  hipLaunchKernelGGL(bias_add_kernel, dim3(grid_for((long long)rows * cols)), dim3(256), 0, s, z, b, rows, cols);
+  return hipGetLastError();
+}
+
+hipError_t relu_launch(hipStream_t s, const float* x, float* y, size_t n) {
+  hipLaunchKernelGGL(relu_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, x, y, (long long)n);
+  return hipGetLastError();
+}
+
+hipError_t relu_bwd_launch(hipStream_t s, const void* a, int a_dtype, float* delta, size_t n) {
+  if (a_dtype == RT_F32)
+    hipLaunchKernelGGL(relu_bwd_kernel<float>, dim3(grid_for((long long)n)), dim3(256), 0, s,
+                       static_cast<const float*>(a), delta, (long long)n);
+  else if (a_dtype == RT_BF16)
+    hipLaunchKernelGGL(relu_bwd_kernel<unsigned short>, dim3(grid_for((long long)n)), dim3(256), 0, s,
+                       static_cast<const unsigned short*>(a), delta, (long long)n);
+  else
+    hipLaunchKernelGGL(relu_bwd_kernel<_Float16>, dim3(grid_for((long long)n)), dim3(256), 0, s,
+                       static_cast<const _Float16*>(a), delta, (long long)n);
+  return hipGetLastError();
+}
+
+hipError_t convert_launch(hipStream_t s, const void* src, int src_dtype, void* dst, int dst_dtype, size_t n) {
+  hipLaunchKernelGGL(convert_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, src, src_dtype, dst, dst_dtype,
+                     (long long)n);
+  return hipGetLastError();
+}
+
+hipError_t fill_i32_launch(hipStream_t s, int* p, int v, size_t n) {
+  hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, p, v, (long long)n);
+  return hipGetLastError();
+}
+
+}  // namespace rt

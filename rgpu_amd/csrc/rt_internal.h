@@ -1,0 +1,130 @@
+// Internal declarations shared by the host runtime and the kernel sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "rtensor_hip.h"
+
+struct rt_buf {
+  void* ptr = nullptr;
+  rt_dtype dtype = RT_F32;
+  size_t shape[4] = {0, 0, 0, 0};
+  int rank = 0;
+  size_t n = 0;      // elements
+  size_t bytes = 0;  // n * element size
+};
+
+struct rt_prof_rec {
+  std::string label;
+  hipEvent_t e0, e1;
+};
+
+struct rt_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string err;
+  std::string arch;
+  std::string name;
+  int num_cus = 0;
+  // Device flags written by kernels: [0] label out of range, [1] non-finite
+  // gradient.  Zeroed by a fill kernel, read back by the blocking readers.
+  int* d_flags = nullptr;
+  // Grow-only device scratch for ops that need temporaries (colsum stage 1).
+  float* scratch = nullptr;
+  size_t scratch_elems = 0;
+  bool profiling = false;
+  std::vector<rt_prof_rec> prof;
+  std::vector<hipEvent_t> event_pool;
+};
+
+namespace rt {
+
+size_t dtype_size(rt_dtype d);
+int fail(rt_ctx* c, int code, const char* fmt, ...);
+int hip_fail(rt_ctx* c, hipError_t e, const char* what);
+
+// Brackets one kernel launch with HIP events when profiling is on.
+class Launch {
+ public:
+  Launch(rt_ctx* c, const char* label);
+  ~Launch();
+  Launch(const Launch&) = delete;
+  Launch& operator=(const Launch&) = delete;
+
+ private:
+  rt_ctx* c_;
+  const char* label_;
+  hipEvent_t e0_ = nullptr;
+};
+
+// ---------------------------------------------------------------- GEMM
+struct GemmDesc {
+  int layout = RT_NN;        // rt_layout
+  int in_dtype = RT_F32;     // dtype of A and B
+  int out_dtype = RT_F32;    // dtype of C (f32, or bf16 for half inputs)
+  const void* A = nullptr;
+  const void* B = nullptr;
+  void* C = nullptr;
+  int M = 0, N = 0, K = 0;
+  int lda = 0, ldb = 0, ldc = 0;  // leading dimensions in elements
+  int epi = RT_EPI_NONE;
+  const float* bias = nullptr;    // [N] f32
+  const void* mask = nullptr;     // [M, N], ld = ldc, dtype = mask_dtype
+  int mask_dtype = RT_F32;
+  float* colsum = nullptr;        // [N] f32 = 1ᵀ·B over this launch's K range
+  int splits = 1;                 // K slices (blockIdx.z); >1 writes f32 partial planes
+  long long split_stride = 0;     // elements between partial planes of C
+  float* colsum_partials = nullptr;  // [splits, N] when splits > 1
+};
+
+// Enqueues C (or its partial planes) on stream.  Shapes and pointers are
+// validated by the caller.
+hipError_t gemm_launch(hipStream_t s, const GemmDesc& d);
+// Sums `splits` f32 partial planes of [M, N] in slice order into C and applies
+// the epilogue; also sums colsum partials [splits, N] into colsum if given.
+hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M,
+                                int N, void* C, int out_dtype, int ldc, int epi, const float* bias,
+                                const void* mask, int mask_dtype, const float* colsum_partials, float* colsum);
+
+// ---------------------------------------------------------------- row / column kernels
+hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, int cols, float* dst,
+                         float* scratch, size_t scratch_elems);
+size_t colsum_scratch_elems(int rows, int cols);
+hipError_t bias_add_launch(hipStream_t s, float* z, const float* b, int rows, int cols);
+hipError_t relu_launch(hipStream_t s, const float* x, float* y, size_t n);
+hipError_t relu_bwd_launch(hipStream_t s, const void* a, int a_dtype, float* delta, size_t n);
+hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* labels, float* delta, void* delta_half,
+                       float* loss_rows, int rows, int cols, float scale, int* err_flag);
+hipError_t convert_launch(hipStream_t s, const void* src, int src_dtype, void* dst, int dst_dtype, size_t n);
+hipError_t fill_i32_launch(hipStream_t s, int* p, int v, size_t n);
+
+// ---------------------------------------------------------------- optimizer
+struct OptTensor {
+  float* theta;       // f32 parameter (master copy under mixed precision)
+  const float* grad;  // f32 gradient
+  float* m;           // Adam first moment / SGD velocity (nullable for plain SGD)
+  float* v;           // Adam second moment
+  void* half_copy;    // optional bf16 copy of theta written after the update
+  size_t n;
+};
+struct OptParams {
+  int kind = 0;  // 0 Adam, 1 SGD
+  float lr = 0, beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, momentum = 0;
+  float inv_c1 = 1, inv_c2 = 1;  // Adam bias corrections, 1/(1-β^t) in f32
+  float grad_scale = 1;          // multiplies g first (1/loss_scale), exact for powers of two
+  const int* skip_flag = nullptr;  // if non-null and *skip_flag != 0, the update is skipped
+};
+constexpr int kMaxOptTensors = 24;
+hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const OptParams& p);
+// Sets *flag = 1 if any of the n floats of any tensor is not finite.
+hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag);
+
+// f32 powi as rtensor's Adam computes β^t (square-and-multiply).
+float powi_f32(float a, int b);
+
+}  // namespace rt

@@ -1,0 +1,633 @@
+// Host runtime of the C ABI: device context, buffers, transfers, argument
+// validation and the op-level entry points (rtensor::gpu::Gpu, mod.rs:224-1237).
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+
+#include "rt_internal.h"
+
+namespace rt {
+
+hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d);
+hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d);
+
+hipError_t gemm_launch(hipStream_t s, const GemmDesc& d) {
+  if (d.in_dtype == RT_F32) return gemm_f32_launch(s, d);
+  return gemm_half_launch(s, d);
+}
+
+size_t dtype_size(rt_dtype d) {
+  switch (d) {
+    case RT_F32: return 4;
+    case RT_BF16: return 2;
+    case RT_F16: return 2;
+    case RT_U32: return 4;
+  }
+  return 0;
+}
+
+int fail(rt_ctx* c, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (c) c->err = buf;
+  return code;
+}
+
+int hip_fail(rt_ctx* c, hipError_t e, const char* what) {
+  return fail(c, e == hipErrorOutOfMemory ? RT_ERR_OOM : RT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+Launch::Launch(rt_ctx* c, const char* label) : c_(c), label_(label) {
+  if (!c_->profiling) return;
+  if (c_->event_pool.empty()) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    c_->event_pool.push_back(e);
+  }
+  e0_ = c_->event_pool.back();
+  c_->event_pool.pop_back();
+  hipEventRecord(e0_, c_->stream);
+}
+
+Launch::~Launch() {
+  if (!c_->profiling || e0_ == nullptr) return;
+  hipEvent_t e1;
+  if (c_->event_pool.empty()) {
+    if (hipEventCreate(&e1) != hipSuccess) {
+      c_->event_pool.push_back(e0_);
+      return;
+    }
+  } else {
+    e1 = c_->event_pool.back();
+    c_->event_pool.pop_back();
+  }
+  hipEventRecord(e1, c_->stream);
+  c_->prof.push_back(rt_prof_rec{std::string(label_), e0_, e1});
+}
+
+}  // namespace rt
+
+using namespace rt;
+
+static std::string g_open_err;
+
+#define CHECK_CTX(c)                                       \
+  do {                                                     \
+    if ((c) == nullptr) return RT_ERR_INVALID;             \
+  } while (0)
+
+#define HIP_TRY(c, expr, what)                             \
+  do {                                                     \
+    hipError_t _e = (expr);                                \
+    if (_e != hipSuccess) return hip_fail((c), _e, what);  \
+  } while (0)
+
+static bool is_half(rt_dtype d) { return d == RT_BF16 || d == RT_F16; }
+static size_t cols_of(const rt_buf* b) { return b->rank >= 2 ? b->shape[b->rank - 1] : b->n; }
+
+extern "C" {
+
+int rt_open(int device, rt_ctx** out) {
+  if (out == nullptr) return RT_ERR_INVALID;
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0) {
+    g_open_err = std::string("no HIP device: ") + (e != hipSuccess ? hipGetErrorString(e) : "count is 0");
+    return RT_ERR_NO_DEVICE;
+  }
+  if (device < 0 || device >= count) {
+    g_open_err = "device ordinal out of range";
+    return RT_ERR_NO_DEVICE;
+  }
+  e = hipSetDevice(device);
+  if (e != hipSuccess) {
+    g_open_err = std::string("hipSetDevice: ") + hipGetErrorString(e);
+    return RT_ERR_NO_DEVICE;
+  }
+  hipDeviceProp_t props;
+  e = hipGetDeviceProperties(&props, device);
+  if (e != hipSuccess) {
+    g_open_err = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+    return RT_ERR_NO_DEVICE;
+  }
+  std::string arch = props.gcnArchName;
+  if (arch.rfind("gfx950", 0) != 0) {
+    g_open_err = "unsupported device arch " + arch + " (this library is built for gfx950)";
+    return RT_ERR_NO_DEVICE;
+  }
+  auto* c = new rt_ctx();
+  c->device = device;
+  c->arch = arch;
+  c->name = props.name;
+  c->num_cus = props.multiProcessorCount;
+  e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipMalloc(&c->d_flags, 64 * sizeof(int));
+  if (e == hipSuccess) e = fill_i32_launch(c->stream, c->d_flags, 0, 64);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) {
+    g_open_err = std::string("context setup: ") + hipGetErrorString(e);
+    if (c->d_flags) hipFree(c->d_flags);
+    if (c->stream) hipStreamDestroy(c->stream);
+    delete c;
+    return RT_ERR_HIP;
+  }
+  *out = c;
+  return RT_OK;
+}
+
+int rt_close(rt_ctx* c) {
+  CHECK_CTX(c);
+  hipSetDevice(c->device);
+  hipStreamSynchronize(c->stream);
+  for (auto& r : c->prof) {
+    hipEventDestroy(r.e0);
+    hipEventDestroy(r.e1);
+  }
+  for (auto e : c->event_pool) hipEventDestroy(e);
+  hipFree(c->d_flags);
+  if (c->scratch) hipFree(c->scratch);
+  hipStreamDestroy(c->stream);
+  delete c;
+  return RT_OK;
+}
+
+const char* rt_last_error(const rt_ctx* c) { return c ? c->err.c_str() : g_open_err.c_str(); }
+
+int rt_info(rt_ctx* c, char* buf, size_t len) {
+  CHECK_CTX(c);
+  if (buf == nullptr || len == 0) return RT_ERR_INVALID;
+  snprintf(buf, len, "%s (%s, %d CUs)", c->name.c_str(), c->arch.c_str(), c->num_cus);
+  return RT_OK;
+}
+
+int rt_sync(rt_ctx* c) {
+  CHECK_CTX(c);
+  int flag = 0;
+  HIP_TRY(c, hipMemcpyAsync(&flag, c->d_flags, sizeof(int), hipMemcpyDeviceToHost, c->stream), "flag read");
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+  if (flag != 0) {
+    // The label flag is sticky until reported once.
+    HIP_TRY(c, fill_i32_launch(c->stream, c->d_flags, 0, 1), "flag reset");
+    HIP_TRY(c, hipStreamSynchronize(c->stream), "flag reset sync");
+    return fail(c, RT_ERR_LABEL, "a label was >= the number of classes");
+  }
+  return RT_OK;
+}
+
+static int make_buf(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out) {
+  if (out == nullptr || (rank > 0 && shape == nullptr) || rank < 0 || rank > 4)
+    return fail(c, RT_ERR_INVALID, "bad shape arguments");
+  if (dtype < RT_F32 || dtype > RT_U32) return fail(c, RT_ERR_DTYPE, "unknown dtype %d", (int)dtype);
+  auto* b = new rt_buf();
+  b->dtype = dtype;
+  b->rank = rank;
+  size_t n = 1;
+  for (int i = 0; i < rank; ++i) {
+    b->shape[i] = shape[i];
+    n *= shape[i];
+  }
+  b->n = n;
+  b->bytes = n * dtype_size(dtype);
+  if (b->bytes > 0) {
+    // Whole 4-byte words, so zero fills never need a byte memset.
+    hipError_t e = hipMalloc(&b->ptr, (b->bytes + 3) / 4 * 4);
+    if (e != hipSuccess) {
+      delete b;
+      return hip_fail(c, e, "hipMalloc");
+    }
+  }
+  *out = b;
+  return RT_OK;
+}
+
+int rt_zeros(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out) {
+  CHECK_CTX(c);
+  int rc = make_buf(c, dtype, shape, rank, out);
+  if (rc != RT_OK) return rc;
+  rt_buf* b = *out;
+  if (b->bytes > 0) {
+    // Zero fill with a kernel, not a memset node (graph-capture safe).
+    size_t words = (b->bytes + 3) / 4;
+    hipError_t e = fill_i32_launch(c->stream, static_cast<int*>(b->ptr), 0, words);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+      hipFree(b->ptr);
+      delete b;
+      *out = nullptr;
+      return hip_fail(c, e, "zero fill");
+    }
+  }
+  return RT_OK;
+}
+
+int rt_upload(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, const void* host, rt_buf** out) {
+  CHECK_CTX(c);
+  int rc = make_buf(c, dtype, shape, rank, out);
+  if (rc != RT_OK) return rc;
+  rt_buf* b = *out;
+  if (b->bytes > 0) {
+    if (host == nullptr) {
+      hipFree(b->ptr);
+      delete b;
+      *out = nullptr;
+      return fail(c, RT_ERR_INVALID, "null host pointer");
+    }
+    hipError_t e = hipMemcpyAsync(b->ptr, host, b->bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+      hipFree(b->ptr);
+      delete b;
+      *out = nullptr;
+      return hip_fail(c, e, "upload");
+    }
+  }
+  return RT_OK;
+}
+
+int rt_download(rt_ctx* c, const rt_buf* b, void* host, size_t bytes) {
+  CHECK_CTX(c);
+  if (b == nullptr || (host == nullptr && b->bytes > 0)) return fail(c, RT_ERR_INVALID, "null argument");
+  if (bytes != b->bytes) return fail(c, RT_ERR_SHAPE, "download of %zu bytes from a %zu-byte tensor", bytes, b->bytes);
+  if (b->bytes == 0) return RT_OK;
+  HIP_TRY(c, hipMemcpyAsync(host, b->ptr, b->bytes, hipMemcpyDeviceToHost, c->stream), "download");
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "download sync");
+  return RT_OK;
+}
+
+int rt_write(rt_ctx* c, rt_buf* b, const void* host, size_t bytes) {
+  CHECK_CTX(c);
+  if (b == nullptr || (host == nullptr && bytes > 0)) return fail(c, RT_ERR_INVALID, "null argument");
+  if (bytes != b->bytes) return fail(c, RT_ERR_SHAPE, "write of %zu bytes into a %zu-byte tensor", bytes, b->bytes);
+  if (bytes == 0) return RT_OK;
+  HIP_TRY(c, hipMemcpyAsync(b->ptr, host, bytes, hipMemcpyHostToDevice, c->stream), "write");
+  // The host buffer is caller-owned and may be reused on return.
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "write sync");
+  return RT_OK;
+}
+
+int rt_free(rt_ctx* c, rt_buf* b) {
+  CHECK_CTX(c);
+  if (b == nullptr) return RT_OK;
+  // Work already enqueued may still read the buffer.
+  hipStreamSynchronize(c->stream);
+  if (b->ptr) hipFree(b->ptr);
+  delete b;
+  return RT_OK;
+}
+
+int rt_buf_info(const rt_buf* b, rt_dtype* dtype, size_t* shape, int* rank) {
+  if (b == nullptr) return RT_ERR_INVALID;
+  if (dtype) *dtype = b->dtype;
+  if (rank) *rank = b->rank;
+  if (shape)
+    for (int i = 0; i < b->rank; ++i) shape[i] = b->shape[i];
+  return RT_OK;
+}
+
+int rt_upload_labels(rt_ctx* c, const uint64_t* labels, size_t n, rt_buf** out) {
+  CHECK_CTX(c);
+  if (labels == nullptr && n > 0) return fail(c, RT_ERR_INVALID, "null labels");
+  std::vector<uint32_t> v(n);
+  for (size_t i = 0; i < n; ++i) {
+    if (labels[i] > 0xffffffffULL) return fail(c, RT_ERR_LABEL, "label %zu does not fit u32", i);
+    v[i] = (uint32_t)labels[i];
+  }
+  size_t shape[1] = {n};
+  return rt_upload(c, RT_U32, shape, 1, v.data(), out);
+}
+
+int rt_convert(rt_ctx* c, const rt_buf* src, rt_buf* dst) {
+  CHECK_CTX(c);
+  if (!src || !dst) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (src->n != dst->n) return fail(c, RT_ERR_SHAPE, "convert: %zu vs %zu elements", src->n, dst->n);
+  if (src->dtype == RT_U32 || dst->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "convert: u32 not supported");
+  Launch L(c, "convert");
+  HIP_TRY(c, convert_launch(c->stream, src->ptr, src->dtype, dst->ptr, dst->dtype, src->n), "convert");
+  return RT_OK;
+}
+
+// ------------------------------------------------------------------ GEMM
+static int gemm_shapes(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, size_t* M, size_t* N,
+                       size_t* K) {
+  if (a->rank != 2 || b->rank != 2) return fail(c, RT_ERR_SHAPE, "gemm operands must be rank 2");
+  size_t am = a->shape[0], ak = a->shape[1], bk = b->shape[0], bn = b->shape[1];
+  switch (layout) {
+    case RT_NN: *M = am; *K = ak; *N = bn; if (bk != ak) goto bad; break;
+    case RT_TN: *K = am; *M = ak; *N = bn; if (bk != am) goto bad; break;   // A stored [K, M]
+    case RT_NT: *M = am; *K = ak; *N = bk; if (bn != ak) goto bad; break;   // B stored [N, K]
+    default: return fail(c, RT_ERR_INVALID, "unknown layout %d", (int)layout);
+  }
+  if (*M > 0x7fffffff || *N > 0x7fffffff || *K > 0x7fffffff) return fail(c, RT_ERR_SHAPE, "dimension too large");
+  return RT_OK;
+bad:
+  return fail(c, RT_ERR_SHAPE, "gemm inner dimensions differ: [%zu,%zu] x [%zu,%zu] (layout %d)", am, ak, bk, bn,
+              (int)layout);
+}
+
+static int check_epilogue(rt_ctx* c, rt_epilogue epi, const rt_buf* aux, const rt_buf* out, size_t M, size_t N) {
+  if (epi == RT_EPI_NONE) return RT_OK;
+  if (aux == nullptr) return fail(c, RT_ERR_INVALID, "epilogue needs an aux buffer");
+  if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) {
+    if (aux->dtype != RT_F32 || aux->n != N) return fail(c, RT_ERR_SHAPE, "bias must be f32 with %zu elements", N);
+  } else if (epi == RT_EPI_RELU_MASK) {
+    if (aux->n != M * N || aux->dtype == RT_U32) return fail(c, RT_ERR_SHAPE, "mask must match C [%zu,%zu]", M, N);
+    if (aux->dtype != out->dtype && !(out->dtype == RT_F32 && aux->dtype == RT_F32))
+      return fail(c, RT_ERR_DTYPE, "mask dtype must match C");
+  } else {
+    return fail(c, RT_ERR_INVALID, "unknown epilogue %d", (int)epi);
+  }
+  return RT_OK;
+}
+
+int rt_gemm(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, rt_epilogue epi,
+            const rt_buf* aux, rt_buf* colsum) {
+  CHECK_CTX(c);
+  if (!a || !b || !out) return fail(c, RT_ERR_INVALID, "null buffer");
+  size_t M, N, K;
+  int rc = gemm_shapes(c, layout, a, b, &M, &N, &K);
+  if (rc) return rc;
+  if (out->n != M * N || (out->rank == 2 && (out->shape[0] != M || out->shape[1] != N)))
+    return fail(c, RT_ERR_SHAPE, "C must be [%zu,%zu]", M, N);
+  if (a->dtype != b->dtype || a->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "A and B must share a float dtype");
+  if (a->dtype == RT_F32 && out->dtype != RT_F32) return fail(c, RT_ERR_DTYPE, "f32 GEMM writes f32");
+  if (is_half(a->dtype) && !(out->dtype == RT_F32 || out->dtype == RT_BF16))
+    return fail(c, RT_ERR_DTYPE, "half GEMM writes f32 or bf16");
+  if ((rc = check_epilogue(c, epi, aux, out, M, N))) return rc;
+  if (colsum) {
+    if (layout != RT_TN) return fail(c, RT_ERR_INVALID, "fused colsum is only for the TN layout");
+    if (colsum->dtype != RT_F32 || colsum->n != N) return fail(c, RT_ERR_SHAPE, "colsum must be f32 [%zu]", N);
+  }
+  if (M == 0 || N == 0) return RT_OK;
+  GemmDesc d;
+  d.layout = layout;
+  d.in_dtype = a->dtype;
+  d.out_dtype = out->dtype;
+  d.A = a->ptr;
+  d.B = b->ptr;
+  d.C = out->ptr;
+  d.M = (int)M;
+  d.N = (int)N;
+  d.K = (int)K;
+  d.lda = (int)a->shape[1];
+  d.ldb = (int)b->shape[1];
+  d.ldc = (int)N;
+  d.epi = epi;
+  if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) d.bias = static_cast<const float*>(aux->ptr);
+  if (epi == RT_EPI_RELU_MASK) {
+    d.mask = aux->ptr;
+    d.mask_dtype = aux->dtype;
+  }
+  d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
+  Launch L(c, layout == RT_NN ? "gemm_nn" : layout == RT_TN ? "gemm_tn" : "gemm_nt");
+  HIP_TRY(c, gemm_launch(c->stream, d), "gemm launch");
+  return RT_OK;
+}
+
+size_t rt_splitk_slices(size_t m, size_t n, size_t k) {
+  // Split only when the output tiles alone cannot fill the 256 CUs: aim for
+  // ~512 workgroups (two per CU), keep at least 4 K steps of 32 per slice,
+  // and cap at 32 slices so the partial planes stay small next to A and B.
+  const size_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
+  const size_t ksteps = (k + 31) / 32;
+  if (tiles >= 256 || ksteps < 8) return 1;
+  size_t s = std::min<size_t>(512 / tiles, ksteps / 4);
+  s = std::min<size_t>(s, 32);
+  return std::max<size_t>(s, 1);
+}
+
+int rt_gemm_splitk(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, rt_buf* partials,
+                   size_t slices, rt_buf* colsum) {
+  CHECK_CTX(c);
+  if (!a || !b || !out || !partials) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (layout != RT_NN && layout != RT_TN) return fail(c, RT_ERR_INVALID, "split-K takes RT_NN or RT_TN");
+  if (slices < 1 || slices > 1024) return fail(c, RT_ERR_INVALID, "slices must be in [1, 1024]");
+  size_t M, N, K;
+  int rc = gemm_shapes(c, layout, a, b, &M, &N, &K);
+  if (rc) return rc;
+  if (out->n != M * N || out->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "C must be f32 [%zu,%zu]", M, N);
+  if (a->dtype != b->dtype || a->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "A and B must share a float dtype");
+  if (partials->dtype != RT_F32 || partials->n < slices * M * N + (colsum ? slices * N : 0))
+    return fail(c, RT_ERR_SHAPE, "partials need %zu f32 elements", slices * M * N + (colsum ? slices * N : 0));
+  if (colsum) {
+    if (layout != RT_TN) return fail(c, RT_ERR_INVALID, "fused colsum is only for the TN layout");
+    if (colsum->dtype != RT_F32 || colsum->n != N) return fail(c, RT_ERR_SHAPE, "colsum must be f32 [%zu]", N);
+  }
+  if (M == 0 || N == 0) return RT_OK;
+  GemmDesc d;
+  d.layout = layout;
+  d.in_dtype = a->dtype;
+  d.out_dtype = RT_F32;
+  d.A = a->ptr;
+  d.B = b->ptr;
+  d.M = (int)M;
+  d.N = (int)N;
+  d.K = (int)K;
+  d.lda = (int)a->shape[1];
+  d.ldb = (int)b->shape[1];
+  d.ldc = (int)N;
+  float* part = static_cast<float*>(partials->ptr);
+  if (slices == 1) {
+    d.C = out->ptr;
+    d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
+    Launch L(c, "splitk_gemm");
+    HIP_TRY(c, gemm_launch(c->stream, d), "split-K gemm");
+    return RT_OK;
+  }
+  d.C = part;
+  d.splits = (int)slices;
+  d.split_stride = (long long)(M * N);
+  d.colsum_partials = colsum ? part + slices * M * N : nullptr;
+  {
+    Launch L(c, "splitk_gemm");
+    HIP_TRY(c, gemm_launch(c->stream, d), "split-K gemm");
+  }
+  Launch L(c, "splitk_reduce");
+  HIP_TRY(c,
+          splitk_reduce_launch(c->stream, part, (int)slices, (long long)(M * N), (int)M, (int)N, out->ptr, RT_F32,
+                               (int)N, RT_EPI_NONE, nullptr, nullptr, RT_F32, d.colsum_partials,
+                               colsum ? static_cast<float*>(colsum->ptr) : nullptr),
+          "split-K reduce");
+  return RT_OK;
+}
+
+// ------------------------------------------------------------------ row / column ops
+int rt_colsum(rt_ctx* c, const rt_buf* src, rt_buf* dst) {
+  CHECK_CTX(c);
+  if (!src || !dst) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (src->rank != 2) return fail(c, RT_ERR_SHAPE, "colsum source must be rank 2");
+  size_t R = src->shape[0], Cc = src->shape[1];
+  if (dst->dtype != RT_F32 || dst->n != Cc) return fail(c, RT_ERR_SHAPE, "colsum target must be f32 [1,%zu]", Cc);
+  if (src->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "colsum of u32");
+  size_t se = colsum_scratch_elems((int)R, (int)Cc);
+  if (se > c->scratch_elems) {
+    // Grow the context scratch; earlier work may still read the old one.
+    HIP_TRY(c, hipStreamSynchronize(c->stream), "scratch sync");
+    if (c->scratch) hipFree(c->scratch);
+    c->scratch = nullptr;
+    c->scratch_elems = 0;
+    HIP_TRY(c, hipMalloc((void**)&c->scratch, se * sizeof(float)), "colsum scratch");
+    c->scratch_elems = se;
+  }
+  Launch L(c, "colsum");
+  HIP_TRY(c, colsum_launch(c->stream, src->ptr, src->dtype, (int)R, (int)Cc, static_cast<float*>(dst->ptr), c->scratch,
+                           c->scratch_elems),
+          "colsum");
+  return RT_OK;
+}
+
+int rt_bias_add(rt_ctx* c, rt_buf* z, const rt_buf* b) {
+  CHECK_CTX(c);
+  if (!z || !b) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (z->dtype != RT_F32 || b->dtype != RT_F32) return fail(c, RT_ERR_DTYPE, "bias_add is f32");
+  size_t cols = cols_of(z);
+  if (b->n != cols || z->n % std::max<size_t>(cols, 1)) return fail(c, RT_ERR_SHAPE, "bias must have %zu elements", cols);
+  if (z->n == 0) return RT_OK;
+  Launch L(c, "bias_add");
+  HIP_TRY(c, bias_add_launch(c->stream, static_cast<float*>(z->ptr), static_cast<const float*>(b->ptr),
+                             (int)(z->n / cols), (int)cols),
+          "bias_add");
+  return RT_OK;
+}
+
+int rt_relu(rt_ctx* c, const rt_buf* x, rt_buf* y) {
+  CHECK_CTX(c);
+  if (!x || !y) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (x->dtype != RT_F32 || y->dtype != RT_F32 || x->n != y->n) return fail(c, RT_ERR_SHAPE, "relu: f32, same size");
+  if (x->n == 0) return RT_OK;
+  Launch L(c, "relu");
+  HIP_TRY(c, relu_launch(c->stream, static_cast<const float*>(x->ptr), static_cast<float*>(y->ptr), x->n), "relu");
+  return RT_OK;
+}
+
+int rt_relu_bwd(rt_ctx* c, const rt_buf* a, rt_buf* delta) {
+  CHECK_CTX(c);
+  if (!a || !delta) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (delta->dtype != RT_F32 || a->dtype == RT_U32 || a->n != delta->n)
+    return fail(c, RT_ERR_SHAPE, "relu_bwd: delta f32, same size as a");
+  if (a->n == 0) return RT_OK;
+  Launch L(c, "relu_bwd");
+  HIP_TRY(c, relu_bwd_launch(c->stream, a->ptr, a->dtype, static_cast<float*>(delta->ptr), a->n), "relu_bwd");
+  return RT_OK;
+}
+
+int rt_softmax_xent(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, rt_buf* delta, rt_buf* loss_rows,
+                    float scale) {
+  CHECK_CTX(c);
+  if (!logits || !labels || !delta || !loss_rows) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (logits->rank != 2 || logits->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "logits must be f32 [B, C]");
+  size_t B = logits->shape[0], Cc = logits->shape[1];
+  if (labels->dtype != RT_U32 || labels->n != B) return fail(c, RT_ERR_SHAPE, "labels must be u32 [%zu]", B);
+  if (delta->dtype != RT_F32 || delta->n != B * Cc) return fail(c, RT_ERR_SHAPE, "delta must be f32 [%zu,%zu]", B, Cc);
+  if (loss_rows->dtype != RT_F32 || loss_rows->n != B) return fail(c, RT_ERR_SHAPE, "loss_rows must be f32 [%zu]", B);
+  if (Cc == 0) return fail(c, RT_ERR_SHAPE, "zero classes");
+  if (B == 0) return RT_OK;
+  Launch L(c, "softmax_xent");
+  HIP_TRY(c,
+          xent_launch(c->stream, static_cast<const float*>(logits->ptr), static_cast<const uint32_t*>(labels->ptr),
+                      static_cast<float*>(delta->ptr), nullptr, static_cast<float*>(loss_rows->ptr), (int)B, (int)Cc,
+                      scale / (float)B, c->d_flags),
+          "softmax_xent");
+  return RT_OK;
+}
+
+int rt_adam(rt_ctx* c, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, float lr, float beta1, float beta2,
+            float eps, int t) {
+  CHECK_CTX(c);
+  if (!theta || !m || !v || !g) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (theta->dtype != RT_F32 || m->dtype != RT_F32 || v->dtype != RT_F32 || g->dtype != RT_F32)
+    return fail(c, RT_ERR_DTYPE, "adam is f32");
+  if (m->n != theta->n || v->n != theta->n || g->n != theta->n) return fail(c, RT_ERR_SHAPE, "adam: sizes differ");
+  if (t < 1) return fail(c, RT_ERR_INVALID, "adam step t must be >= 1");
+  OptTensor T{static_cast<float*>(theta->ptr), static_cast<const float*>(g->ptr), static_cast<float*>(m->ptr),
+              static_cast<float*>(v->ptr), nullptr, theta->n};
+  OptParams P;
+  P.kind = 0;
+  P.lr = lr;
+  P.beta1 = beta1;
+  P.beta2 = beta2;
+  P.eps = eps;
+  float c1 = 1.0f - powi_f32(beta1, t), c2 = 1.0f - powi_f32(beta2, t);
+  P.inv_c1 = 1.0f / c1;
+  P.inv_c2 = 1.0f / c2;
+  Launch L(c, "optimizer");
+  HIP_TRY(c, optimizer_launch(c->stream, &T, 1, P), "adam");
+  return RT_OK;
+}
+
+int rt_sgd(rt_ctx* c, rt_buf* theta, rt_buf* velocity, const rt_buf* g, float lr, float momentum) {
+  CHECK_CTX(c);
+  if (!theta || !g) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (theta->dtype != RT_F32 || g->dtype != RT_F32) return fail(c, RT_ERR_DTYPE, "sgd is f32");
+  if (g->n != theta->n) return fail(c, RT_ERR_SHAPE, "sgd: sizes differ");
+  if (momentum != 0.0f && (velocity == nullptr || velocity->n != theta->n || velocity->dtype != RT_F32))
+    return fail(c, RT_ERR_INVALID, "sgd with momentum needs an f32 velocity buffer");
+  OptTensor T{static_cast<float*>(theta->ptr), static_cast<const float*>(g->ptr),
+              velocity ? static_cast<float*>(velocity->ptr) : nullptr, nullptr, nullptr, theta->n};
+  OptParams P;
+  P.kind = 1;
+  P.lr = lr;
+  P.momentum = momentum;
+  Launch L(c, "optimizer");
+  HIP_TRY(c, optimizer_launch(c->stream, &T, 1, P), "sgd");
+  return RT_OK;
+}
+
+// ------------------------------------------------------------------ profiling
+int rt_profile_enable(rt_ctx* c, int on) {
+  CHECK_CTX(c);
+  c->profiling = on != 0;
+  return RT_OK;
+}
+
+int rt_profile_reset(rt_ctx* c) {
+  CHECK_CTX(c);
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "profile sync");
+  for (auto& r : c->prof) {
+    c->event_pool.push_back(r.e0);
+    c->event_pool.push_back(r.e1);
+  }
+  c->prof.clear();
+  return RT_OK;
+}
+
+int rt_profile_report(rt_ctx* c, char* names, size_t name_len, int* counts, double* ms, int cap, int* n_out) {
+  CHECK_CTX(c);
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "profile sync");
+  std::vector<std::string> order;
+  std::map<std::string, std::pair<int, double>> agg;
+  for (auto& r : c->prof) {
+    float t = 0;
+    HIP_TRY(c, hipEventElapsedTime(&t, r.e0, r.e1), "hipEventElapsedTime");
+    auto it = agg.find(r.label);
+    if (it == agg.end()) {
+      order.push_back(r.label);
+      agg[r.label] = {1, (double)t};
+    } else {
+      it->second.first += 1;
+      it->second.second += t;
+    }
+  }
+  int n = 0;
+  for (auto& lbl : order) {
+    if (n >= cap) break;
+    if (names && name_len) {
+      strncpy(names + (size_t)n * name_len, lbl.c_str(), name_len - 1);
+      names[(size_t)n * name_len + name_len - 1] = 0;
+    }
+    if (counts) counts[n] = agg[lbl].first;
+    if (ms) ms[n] = agg[lbl].second;
+    ++n;
+  }
+  if (n_out) *n_out = n;
+  return RT_OK;
+}
+
+}  // extern "C"

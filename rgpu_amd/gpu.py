@@ -1,0 +1,422 @@
+"""Host-side mirror of ``rtensor::gpu`` over the C ABI of librtensor_hip.so.
+
+Names follow the reference API (crates/rtensor/src/gpu/mod.rs):
+
+=======================  =============================================  ===============
+rtensor::gpu             here                                           mod.rs
+=======================  =============================================  ===============
+Gpu::new                 Gpu()                                          263-277
+Gpu::info                Gpu.info()                                     412
+Gpu::zeros / upload      Gpu.zeros(shape) / Gpu.upload(array)           501-517
+Gpu::download            Gpu.download(t) -> numpy (blocking)            530-544
+Gpu::sync                Gpu.sync()                                     564-566
+op_matmul(_at_b/_a_bt)   Gpu.matmul / matmul_at_b / matmul_a_bt         685-700
+op_matmul_bias           Gpu.matmul_bias(a, w, c, bias, relu)           722-749
+op_matmul_f16            Gpu.matmul(...) on bf16/f16 tensors            1191-1229
+ops_split_k              Gpu.split_k(a, b, c, partials, slices, trans)  1095-1146
+fatias_sugeridas         Gpu.fatias_sugeridas(m, n, k)                  1079-1088
+ops_colsum               Gpu.colsum(src, dst)                           838-855
+op_bias_add / relu(_bwd) Gpu.bias_add / relu / relu_bwd                 752-788
+op_softmax_xent          Gpu.softmax_xent(logits, labels, delta, loss)  791-808
+op_adam (+atualizar)     Gpu.adam(theta, m, v, g, lr, betas, t)         859-907
+upload_labels            upload_labels(gpu, labels)                     1672-1675
+GpuMlp                   GpuMlp.from_params(gpu, params, lote, lr, ...)  1322-1562
+=======================  =============================================  ===============
+
+Misuse that panics in the reference raises ``RtError`` here, carrying the
+rt_status code.  There is no CPU fallback: if librtensor_hip.so is missing or
+no gfx950 device is present, construction fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "librtensor_hip.so")
+
+F32, BF16, F16, U32 = 0, 1, 2, 3
+NN, TN, NT = 0, 1, 2
+EPI_NONE, EPI_BIAS, EPI_BIAS_RELU, EPI_RELU_MASK = 0, 1, 2, 3
+OPT_ADAM, OPT_SGD = 0, 1
+PREC_F32, PREC_BF16 = 0, 1
+
+STATUS = {0: "RT_OK", 1: "RT_ERR_NO_DEVICE", 2: "RT_ERR_INVALID", 3: "RT_ERR_SHAPE", 4: "RT_ERR_DTYPE",
+          5: "RT_ERR_OOM", 6: "RT_ERR_LABEL", 7: "RT_ERR_HIP", 8: "RT_ERR_OVERFLOW"}
+
+# Every symbol include/rtensor_hip.h declares, with its ctypes signature.
+_VP = C.c_void_p
+_SZP = C.POINTER(C.c_size_t)
+SIGNATURES = {
+    "rt_open": (C.c_int, [C.c_int, C.POINTER(_VP)]),
+    "rt_close": (C.c_int, [_VP]),
+    "rt_last_error": (C.c_char_p, [_VP]),
+    "rt_info": (C.c_int, [_VP, C.c_char_p, C.c_size_t]),
+    "rt_sync": (C.c_int, [_VP]),
+    "rt_zeros": (C.c_int, [_VP, C.c_int, _SZP, C.c_int, C.POINTER(_VP)]),
+    "rt_upload": (C.c_int, [_VP, C.c_int, _SZP, C.c_int, _VP, C.POINTER(_VP)]),
+    "rt_download": (C.c_int, [_VP, _VP, _VP, C.c_size_t]),
+    "rt_write": (C.c_int, [_VP, _VP, _VP, C.c_size_t]),
+    "rt_free": (C.c_int, [_VP, _VP]),
+    "rt_buf_info": (C.c_int, [_VP, C.POINTER(C.c_int), _SZP, C.POINTER(C.c_int)]),
+    "rt_upload_labels": (C.c_int, [_VP, C.POINTER(C.c_uint64), C.c_size_t, C.POINTER(_VP)]),
+    "rt_convert": (C.c_int, [_VP, _VP, _VP]),
+    "rt_gemm": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, C.c_int, _VP, _VP]),
+    "rt_gemm_splitk": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, _VP, C.c_size_t, _VP]),
+    "rt_splitk_slices": (C.c_size_t, [C.c_size_t, C.c_size_t, C.c_size_t]),
+    "rt_colsum": (C.c_int, [_VP, _VP, _VP]),
+    "rt_bias_add": (C.c_int, [_VP, _VP, _VP]),
+    "rt_relu": (C.c_int, [_VP, _VP, _VP]),
+    "rt_relu_bwd": (C.c_int, [_VP, _VP, _VP]),
+    "rt_softmax_xent": (C.c_int, [_VP, _VP, _VP, _VP, _VP, C.c_float]),
+    "rt_adam": (C.c_int, [_VP, _VP, _VP, _VP, _VP, C.c_float, C.c_float, C.c_float, C.c_float, C.c_int]),
+    "rt_sgd": (C.c_int, [_VP, _VP, _VP, _VP, C.c_float, C.c_float]),
+    "rt_mlp_create": (C.c_int, [_VP, C.c_int, _SZP, C.POINTER(C.POINTER(C.c_float)),
+                                C.POINTER(C.POINTER(C.c_float)), C.c_size_t, _VP, C.POINTER(_VP)]),
+    "rt_mlp_destroy": (C.c_int, [_VP]),
+    "rt_mlp_step": (C.c_int, [_VP, _VP, _VP]),
+    "rt_mlp_forward": (C.c_int, [_VP, _VP]),
+    "rt_mlp_logits": (C.c_int, [_VP, C.POINTER(C.c_float), C.c_size_t]),
+    "rt_mlp_last_loss": (C.c_int, [_VP, C.POINTER(C.c_float)]),
+    "rt_mlp_weights": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.c_int]),
+    "rt_mlp_grads": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.c_int]),
+    "rt_mlp_dispatches": (C.c_int, [_VP, C.POINTER(C.c_int)]),
+    "rt_mlp_overflow": (C.c_int, [_VP, C.POINTER(C.c_int)]),
+    "rt_profile_enable": (C.c_int, [_VP, C.c_int]),
+    "rt_profile_reset": (C.c_int, [_VP]),
+    "rt_profile_report": (C.c_int, [_VP, C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_double),
+                                    C.c_int, C.POINTER(C.c_int)]),
+}
+
+
+class RtMlpConfig(C.Structure):
+    """``rt_mlp_config`` from include/rtensor_hip.h."""
+    _fields_ = [("optimizer", C.c_int), ("lr", C.c_float), ("beta1", C.c_float), ("beta2", C.c_float),
+                ("eps", C.c_float), ("momentum", C.c_float), ("precision", C.c_int), ("loss_scale", C.c_float)]
+
+
+_lib: Optional[C.CDLL] = None
+
+
+def lib() -> C.CDLL:
+    """Load librtensor_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m rgpu_amd.build`")
+    L = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+class RtError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{STATUS.get(code, code)}: {msg}")
+        self.code = code
+        self.status = STATUS.get(code, str(code))
+
+
+def _np_dtype(dt: int):
+    return {F32: np.float32, BF16: np.uint16, F16: np.float16, U32: np.uint32}[dt]
+
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    """Round-to-nearest-even f32 -> bf16, returned as uint16 bit patterns."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(b) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+class GpuTensor:
+    """``GpuTensor`` (mod.rs:190-208): owns one device buffer."""
+
+    def __init__(self, gpu: "Gpu", handle: int, shape, dtype: int):
+        self.gpu = gpu
+        self.handle = handle
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = dtype
+
+    def __len__(self):
+        return int(np.prod(self.shape)) if self.shape else 1
+
+    @property
+    def len(self) -> int:
+        return len(self)
+
+    def free(self):
+        if self.handle and self.gpu._h:
+            self.gpu._call("rt_free", self.gpu._h, self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Gpu:
+    """``rtensor::gpu::Gpu`` (mod.rs:224-1237): one device, one HIP stream."""
+
+    def __init__(self, device: int = 0):
+        L = lib()
+        h = C.c_void_p()
+        rc = L.rt_open(device, C.byref(h))
+        if rc != 0:
+            raise RtError(rc, L.rt_last_error(None).decode())
+        self._h = h.value
+
+    def close(self):
+        if self._h:
+            lib().rt_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _call(self, name: str, *args) -> int:
+        rc = getattr(lib(), name)(*args)
+        if rc != 0:
+            raise RtError(rc, lib().rt_last_error(self._h).decode())
+        return rc
+
+    # --------------------------------------------------------------- device
+    def info(self) -> str:
+        buf = C.create_string_buffer(256)
+        self._call("rt_info", self._h, buf, 256)
+        return buf.value.decode()
+
+    def sync(self) -> None:
+        self._call("rt_sync", self._h)
+
+    # --------------------------------------------------------------- buffers
+    def zeros(self, shape, dtype: int = F32) -> GpuTensor:
+        shape = tuple(int(s) for s in shape)
+        arr = (C.c_size_t * max(len(shape), 1))(*shape)
+        h = C.c_void_p()
+        self._call("rt_zeros", self._h, dtype, arr, len(shape), C.byref(h))
+        return GpuTensor(self, h.value, shape, dtype)
+
+    def upload(self, a, dtype: Optional[int] = None) -> GpuTensor:
+        """Upload a host array.  dtype BF16 takes f32 values (rounded to
+        nearest even) or uint16 bit patterns; F16 takes anything numpy can
+        cast to float16."""
+        a = np.asarray(a)
+        if dtype is None:
+            dtype = {np.dtype(np.float32): F32, np.dtype(np.float16): F16, np.dtype(np.uint32): U32}.get(a.dtype, F32)
+        if dtype == BF16:
+            host = a if a.dtype == np.uint16 else f32_to_bf16_bits(a)
+        else:
+            host = a.astype(_np_dtype(dtype), copy=False)
+        host = np.ascontiguousarray(host)
+        shape = host.shape
+        arr = (C.c_size_t * max(len(shape), 1))(*shape)
+        h = C.c_void_p()
+        self._call("rt_upload", self._h, dtype, arr, len(shape), host.ctypes.data_as(C.c_void_p), C.byref(h))
+        return GpuTensor(self, h.value, shape, dtype)
+
+    def download(self, t: GpuTensor) -> np.ndarray:
+        out = np.empty(t.shape, _np_dtype(t.dtype))
+        self._call("rt_download", self._h, t.handle, out.ctypes.data_as(C.c_void_p), out.nbytes)
+        return out
+
+    def download_f32(self, t: GpuTensor) -> np.ndarray:
+        a = self.download(t)
+        if t.dtype == BF16:
+            return bf16_bits_to_f32(a)
+        return a.astype(np.float32)
+
+    def write(self, t: GpuTensor, a) -> None:
+        host = np.ascontiguousarray(a, dtype=_np_dtype(t.dtype))
+        self._call("rt_write", self._h, t.handle, host.ctypes.data_as(C.c_void_p), host.nbytes)
+
+    def convert(self, src: GpuTensor, dst: GpuTensor) -> None:
+        self._call("rt_convert", self._h, src.handle, dst.handle)
+
+    # --------------------------------------------------------------- ops
+    def gemm(self, layout: int, a: GpuTensor, b: GpuTensor, c: GpuTensor, epi: int = EPI_NONE,
+             aux: Optional[GpuTensor] = None, colsum: Optional[GpuTensor] = None) -> None:
+        self._call("rt_gemm", self._h, layout, a.handle, b.handle, c.handle, epi,
+                   aux.handle if aux else None, colsum.handle if colsum else None)
+
+    def matmul(self, a, b, c):
+        """C = A·B (op_matmul, mod.rs:685-688)."""
+        self.gemm(NN, a, b, c)
+
+    def matmul_at_b(self, a, b, c, colsum: Optional[GpuTensor] = None):
+        """C = Aᵀ·B with A stored [k, m] (op_matmul_at_b, mod.rs:691-694)."""
+        self.gemm(TN, a, b, c, colsum=colsum)
+
+    def matmul_a_bt(self, a, b, c, relu_mask_from: Optional[GpuTensor] = None):
+        """C = A·Bᵀ with B stored [n, k] (op_matmul_a_bt, mod.rs:697-700),
+        optionally masked by 1[mask > 0] (fused op_relu_bwd)."""
+        if relu_mask_from is None:
+            self.gemm(NT, a, b, c)
+        else:
+            self.gemm(NT, a, b, c, EPI_RELU_MASK, relu_mask_from)
+
+    def matmul_bias(self, a, w, c, bias, relu: bool):
+        """C = X·W + 1ₙb, ReLU optional (op_matmul_bias, mod.rs:722-749)."""
+        self.gemm(NN, a, w, c, EPI_BIAS_RELU if relu else EPI_BIAS, bias)
+
+    @staticmethod
+    def fatias_sugeridas(m: int, n: int, k: int) -> int:
+        return int(lib().rt_splitk_slices(m, n, k))
+
+    def split_k(self, a, b, c, partials, slices: int, transposta: bool, colsum: Optional[GpuTensor] = None):
+        """ops_split_k (mod.rs:1095-1146)."""
+        self._call("rt_gemm_splitk", self._h, TN if transposta else NN, a.handle, b.handle, c.handle,
+                   partials.handle, slices, colsum.handle if colsum else None)
+
+    def colsum(self, src, dst):
+        self._call("rt_colsum", self._h, src.handle, dst.handle)
+
+    def bias_add(self, z, b):
+        self._call("rt_bias_add", self._h, z.handle, b.handle)
+
+    def relu(self, x, y):
+        self._call("rt_relu", self._h, x.handle, y.handle)
+
+    def relu_bwd(self, a, delta):
+        self._call("rt_relu_bwd", self._h, a.handle, delta.handle)
+
+    def softmax_xent(self, logits, labels, delta, loss_rows, scale: float = 1.0):
+        self._call("rt_softmax_xent", self._h, logits.handle, labels.handle, delta.handle, loss_rows.handle, scale)
+
+    def adam(self, theta, m, v, g, lr: float, betas=(0.9, 0.999), t: int = 1, eps: float = 1e-8):
+        self._call("rt_adam", self._h, theta.handle, m.handle, v.handle, g.handle, lr, betas[0], betas[1], eps, t)
+
+    def sgd(self, theta, g, lr: float, momentum: float = 0.0, velocity: Optional[GpuTensor] = None):
+        self._call("rt_sgd", self._h, theta.handle, velocity.handle if velocity else None, g.handle, lr, momentum)
+
+    # --------------------------------------------------------------- profiling
+    def profile(self, on: bool) -> None:
+        self._call("rt_profile_enable", self._h, 1 if on else 0)
+
+    def profile_reset(self) -> None:
+        self._call("rt_profile_reset", self._h)
+
+    def perfilar(self) -> List[tuple]:
+        """Per-label (name, launches, device ms) since the last reset (Gpu::perfilar, mod.rs:1245-1286)."""
+        cap, nl = 256, 64
+        names = C.create_string_buffer(cap * nl)
+        counts = (C.c_int * cap)()
+        ms = (C.c_double * cap)()
+        n = C.c_int()
+        self._call("rt_profile_report", self._h, names, nl, counts, ms, cap, C.byref(n))
+        out = []
+        for i in range(n.value):
+            nm = names.raw[i * nl:(i + 1) * nl].split(b"\0", 1)[0].decode()
+            out.append((nm, counts[i], ms[i]))
+        return out
+
+
+def upload_labels(gpu: Gpu, labels) -> GpuTensor:
+    """upload_labels (mod.rs:1672-1675): integer labels -> u32 device buffer."""
+    lab = np.ascontiguousarray(np.asarray(labels).astype(np.uint64))
+    h = C.c_void_p()
+    gpu._call("rt_upload_labels", gpu._h, lab.ctypes.data_as(C.POINTER(C.c_uint64)), lab.size, C.byref(h))
+    return GpuTensor(gpu, h.value, (lab.size,), U32)
+
+
+class GpuMlp:
+    """``GpuMlp`` (mod.rs:1322-1562): ReLU hidden layers, linear output,
+    softmax cross-entropy, trained entirely on the device."""
+
+    def __init__(self, gpu: Gpu, handle: int, dims: Sequence[int], batch: int):
+        self.gpu = gpu
+        self._h = handle
+        self.dims = list(dims)
+        self.lote = batch
+
+    @classmethod
+    def from_params(cls, gpu: Gpu, params: Sequence[np.ndarray], lote: int, lr: float, optimizer: str = "adam",
+                    betas=(0.9, 0.999), eps: float = 1e-8, momentum: float = 0.0, precision: str = "f32",
+                    loss_scale: float = 1.0) -> "GpuMlp":
+        """Build from host parameters in ``[W1, b1, W2, b2, ...]`` order (mod.rs:1341)."""
+        if len(params) % 2 != 0 or not params:
+            raise ValueError("expected (W, b) pairs")
+        ws = [np.ascontiguousarray(params[i], dtype=np.float32) for i in range(0, len(params), 2)]
+        bs = [np.ascontiguousarray(params[i], dtype=np.float32).reshape(-1) for i in range(1, len(params), 2)]
+        n = len(ws)
+        dims = [ws[0].shape[0]] + [w.shape[1] for w in ws]
+        cfg = RtMlpConfig(OPT_ADAM if optimizer == "adam" else OPT_SGD, lr, betas[0], betas[1], eps, momentum,
+                          PREC_BF16 if precision == "bf16" else PREC_F32, loss_scale)
+        wp = (C.POINTER(C.c_float) * n)(*[w.ctypes.data_as(C.POINTER(C.c_float)) for w in ws])
+        bp = (C.POINTER(C.c_float) * n)(*[b.ctypes.data_as(C.POINTER(C.c_float)) for b in bs])
+        d = (C.c_size_t * (n + 1))(*dims)
+        h = C.c_void_p()
+        gpu._call("rt_mlp_create", gpu._h, n, d, wp, bp, lote, C.byref(cfg), C.byref(h))
+        return cls(gpu, h.value, dims, lote)
+
+    def destroy(self):
+        if self._h:
+            lib().rt_mlp_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+    def step(self, x: GpuTensor, labels: GpuTensor) -> None:
+        self.gpu._call("rt_mlp_step", self._h, x.handle, labels.handle)
+
+    def forward_only(self, x: GpuTensor) -> None:
+        self.gpu._call("rt_mlp_forward", self._h, x.handle)
+
+    def logits(self) -> np.ndarray:
+        out = np.empty((self.lote, self.dims[-1]), np.float32)
+        self.gpu._call("rt_mlp_logits", self._h, out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
+        return out
+
+    def last_loss(self) -> float:
+        v = C.c_float()
+        self.gpu._call("rt_mlp_last_loss", self._h, C.byref(v))
+        return v.value
+
+    def _shapes(self):
+        out = []
+        for l in range(len(self.dims) - 1):
+            out += [(self.dims[l], self.dims[l + 1]), (1, self.dims[l + 1])]
+        return out
+
+    def _fetch(self, fn: str) -> List[np.ndarray]:
+        arrs = [np.empty(s, np.float32) for s in self._shapes()]
+        ptrs = (C.POINTER(C.c_float) * len(arrs))(*[a.ctypes.data_as(C.POINTER(C.c_float)) for a in arrs])
+        self.gpu._call(fn, self._h, ptrs, len(arrs))
+        return arrs
+
+    def weights(self) -> List[np.ndarray]:
+        return self._fetch("rt_mlp_weights")
+
+    def grads(self) -> List[np.ndarray]:
+        return self._fetch("rt_mlp_grads")
+
+    def dispatches_por_passo(self) -> int:
+        v = C.c_int()
+        self.gpu._call("rt_mlp_dispatches", self._h, C.byref(v))
+        return v.value
+
+    def overflow(self) -> bool:
+        v = C.c_int()
+        self.gpu._call("rt_mlp_overflow", self._h, C.byref(v))
+        return bool(v.value)

@@ -1,0 +1,174 @@
+"""Training-step parity of the HIP MLP plan (GpuMlp) against the CPU oracle:
+the reference's own GPU-vs-CPU tests (crates/rtensor/tests/gpu.rs:62-213) and
+the measured configurations (MLP 512-1024-1024-10 at batch 32 with SGD and at
+batch 2048 with Adam for 100 steps)."""
+import time
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from rgpu_amd import gpu as G
+from tests.gpu_common import (glorot_model, kaiming_model, normal_batch, oracle_threads, quadrant_data,
+                              uniform_labels)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    O.set_threads(oracle_threads())
+    g = G.Gpu(0)
+    yield g
+    O.set_threads(1)
+
+
+def cpu_mlp(params, opt, lr, **kw):
+    m = O.CpuMlp(params[0::2], params[1::2])
+    m.set_optimizer(opt, lr, **kw)
+    return m
+
+
+def test_gradients_match_cpu(gpu):  # gpu.rs:62-97
+    x, lab = quadrant_data()
+    params = glorot_model(42, [8, 16, 16, 4])
+    cpu = cpu_mlp(params, "none", 0.0)
+    loss_cpu = cpu.step(x, lab)
+    mlp = G.GpuMlp.from_params(gpu, params, 64, 0.0)
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+    assert abs(loss_cpu - mlp.last_loss()) < 1e-4
+    for i, (gc, gg) in enumerate(zip(cpu.grads(), mlp.grads())):
+        assert O.erro_rel(gc, gg) < 1e-4, (i, O.erro_rel(gc, gg))
+    # lr = 0 leaves the weights untouched
+    for w0, w1 in zip(params, mlp.weights()):
+        assert np.array_equal(w0.reshape(w1.shape), w1)
+
+
+def _trajectory(gpu, x, lab, dims, seed, steps, lr, tol_loss=2e-3, tol_w=2e-3):
+    params = glorot_model(seed, dims)
+    n = x.shape[0]
+    cpu = cpu_mlp(params, "adam", lr)
+    mlp = G.GpuMlp.from_params(gpu, params, n, lr)
+    gx, gy = gpu.upload(x), G.upload_labels(gpu, lab)
+    worst = 0.0
+    loss_cpu = None
+    for step in range(1, steps + 1):
+        loss_cpu = cpu.step(x, lab)
+        mlp.step(gx, gy)
+        d = abs(loss_cpu - mlp.last_loss())
+        worst = max(worst, d)
+        assert d < tol_loss, (step, loss_cpu, d)
+    ew = max(O.erro_rel(a, b) for a, b in zip(cpu.weights(), mlp.weights()))
+    print(f"trajectory {dims} x{n}: max |dloss| {worst:.2e}, final weights erro_rel {ew:.2e}")
+    assert ew < tol_w
+    return loss_cpu, mlp
+
+
+def test_training_follows_cpu_trajectory(gpu):  # gpu.rs:99-139
+    x, lab = quadrant_data()
+    loss, _ = _trajectory(gpu, x, lab, [8, 16, 16, 4], 7, 120, 0.05)
+    assert loss < 0.15
+
+
+def test_narrow_output_layer_uses_split_k_and_follows_cpu(gpu):  # gpu.rs:145-213
+    x, lab = quadrant_data(512, 8)
+    loss, mlp = _trajectory(gpu, x, lab, [8, 128, 4], 7, 60, 0.05)
+    # The plan split the output layer's forward (512x4, K=128 -> no: 4 K steps)
+    # and its dW (128x4, K=512): launches = fwd 1 + fwd_out (1 or 2) + xent 1
+    # + dW per layer (1 or 2 each) + dX 1 + optimizer 1.
+    s_fwd = G.Gpu.fatias_sugeridas(512, 4, 128)
+    s_dw = [G.Gpu.fatias_sugeridas(8, 128, 512), G.Gpu.fatias_sugeridas(128, 4, 512)]
+    assert s_dw[1] > 1, "the narrow dW must be split"
+    want = 1 + (2 if s_fwd > 1 else 1) + 1 + sum(2 if s > 1 else 1 for s in s_dw) + 1 + 1
+    assert mlp.dispatches_por_passo() == want
+    assert loss < 0.2
+
+
+def test_config_batch32_sgd_one_step(gpu):
+    # MLP 512->1024(ReLU)->1024(ReLU)->10, f32, batch 32, X ~ N(0,1), labels
+    # uniform in [0,10), Kaiming-uniform weights, zero biases, SGD lr = 0.01.
+    dims, B = [512, 1024, 1024, 10], 32
+    params = kaiming_model(1, dims)
+    x = normal_batch(101, B, 512)
+    lab = uniform_labels(102, B, 10)
+    cpu = cpu_mlp(params, "sgd", 0.01)
+    loss_cpu = cpu.step(x, lab)
+    mlp = G.GpuMlp.from_params(gpu, params, B, 0.01, optimizer="sgd")
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+    assert abs(loss_cpu - mlp.last_loss()) < 1e-4
+    eg = [O.erro_rel(a, b) for a, b in zip(cpu.grads(), mlp.grads())]
+    ew = [O.erro_rel(a, b) for a, b in zip(cpu.weights(), mlp.weights())]
+    print("batch 32 SGD: grad erro_rel", ["%.1e" % e for e in eg], "weights", ["%.1e" % e for e in ew])
+    assert max(eg) <= 1e-4 and max(ew) <= 1e-4
+
+
+def test_config_batch2048_adam_100_steps(gpu):
+    # MLP 512->1024->1024->10 f32 at batch 2048, Adam(1e-3, 0.9, 0.999, 1e-8),
+    # 100 steps on fresh seeded N(0,1) batches; per-step loss and final weights.
+    dims, B, steps = [512, 1024, 1024, 10], 2048, 100
+    params = kaiming_model(2, dims)
+    cpu = cpu_mlp(params, "adam", 1e-3)
+    mlp = G.GpuMlp.from_params(gpu, params, B, 1e-3)
+    worst, t_cpu, t0 = 0.0, 0.0, time.time()
+    for step in range(steps):
+        x = normal_batch(10_000 + step, B, 512)
+        lab = uniform_labels(20_000 + step, B, 10)
+        gx, gy = gpu.upload(x), G.upload_labels(gpu, lab)
+        mlp.step(gx, gy)
+        c0 = time.time()
+        loss_cpu = cpu.step(x, lab)
+        t_cpu += time.time() - c0
+        d = abs(loss_cpu - mlp.last_loss())
+        worst = max(worst, d)
+        assert d < 2e-3, (step, loss_cpu, d)
+        if step % 20 == 0:
+            print(f"step {step}: loss {loss_cpu:.5f} |d| {d:.2e} ({time.time() - t0:.1f}s)", flush=True)
+    eg = max(O.erro_rel(a, b) for a, b in zip(cpu.grads(), mlp.grads()))
+    ew = max(O.erro_rel(a, b) for a, b in zip(cpu.weights(), mlp.weights()))
+    print(f"batch 2048 Adam x{steps}: max |dloss| {worst:.2e}, last-step grads {eg:.2e}, "
+          f"final weights {ew:.2e}; oracle {t_cpu / steps * 1e3:.0f} ms/step on {oracle_threads()} threads")
+    assert eg <= 1e-4
+    assert ew <= 2e-3
+
+
+def test_forward_only_and_logits(gpu):  # forward_only / logits (mod.rs:1514-1526)
+    dims = [512, 1024, 1024, 10]
+    params = kaiming_model(3, dims)
+    x = normal_batch(7, 256, 512)
+    mlp = G.GpuMlp.from_params(gpu, params, 256, 0.0)
+    mlp.forward_only(gpu.upload(x))
+    got = mlp.logits()
+    cpu = cpu_mlp(params, "none", 0.0)
+    want = cpu.forward(x)
+    assert O.erro_rel(want, got) < 1e-4
+
+
+def test_bad_labels_and_shapes_are_errors(gpu):
+    x, lab = quadrant_data()
+    params = glorot_model(42, [8, 16, 16, 4])
+    mlp = G.GpuMlp.from_params(gpu, params, 64, 0.01)
+    bad = lab.copy()
+    bad[3] = 4
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, bad))
+    with pytest.raises(G.RtError) as e:
+        mlp.last_loss()
+    assert e.value.status == "RT_ERR_LABEL"
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+    assert np.isfinite(mlp.last_loss())  # the flag was cleared once reported
+    with pytest.raises(G.RtError) as e:
+        mlp.step(gpu.upload(x[:32]), G.upload_labels(gpu, lab[:32]))
+    assert e.value.status == "RT_ERR_SHAPE"
+
+
+def test_training_is_deterministic(gpu):
+    x, lab = quadrant_data(512, 8)
+    params = glorot_model(9, [8, 128, 4])
+    outs = []
+    for _ in range(2):
+        mlp = G.GpuMlp.from_params(gpu, params, 512, 0.05)
+        gx, gy = gpu.upload(x), G.upload_labels(gpu, lab)
+        for _ in range(10):
+            mlp.step(gx, gy)
+        outs.append(mlp.weights())
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)

@@ -1,0 +1,284 @@
+"""Op-level parity of the HIP kernels against the CPU oracle
+(crates/rtensor/tests/gpu.rs:215-503 and closed forms)."""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from rgpu_amd import gpu as G
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    g = G.Gpu(0)
+    print("device:", g.info(), flush=True)
+    yield g
+
+
+def sincos(m, k, n, fa=0.013, fb=0.007):
+    a = np.sin(np.arange(m * k, dtype=np.float32) * np.float32(fa)).astype(np.float32).reshape(m, k)
+    b = np.cos(np.arange(k * n, dtype=np.float32) * np.float32(fb)).astype(np.float32).reshape(k, n)
+    return a, b
+
+
+def test_upload_download_roundtrip_is_exact(gpu):  # gpu.rs:215-221
+    t = (np.arange(15, dtype=np.float32) * 0.5 - 3.0).reshape(3, 5)
+    assert np.array_equal(gpu.download(gpu.upload(t)), t)
+    u = np.arange(1000, dtype=np.uint32) * 7919
+    assert np.array_equal(gpu.download(gpu.upload(u)), u)
+    h = np.random.default_rng(0).normal(size=(33, 7)).astype(np.float16)
+    assert np.array_equal(gpu.download(gpu.upload(h)), h)
+    lab = gpu.download(G.upload_labels(gpu, np.array([0, 9, 3, 4294967295], np.uint64)))
+    assert lab.tolist() == [0, 9, 3, 4294967295]
+
+
+def test_matmul_37x19x23(gpu):  # gpu.rs:223-240
+    a = np.sin(np.arange(37 * 23, dtype=np.float32) * np.float32(0.11)).reshape(37, 23)
+    b = np.cos(np.arange(23 * 19, dtype=np.float32) * np.float32(0.07)).reshape(23, 19)
+    c = gpu.zeros((37, 19))
+    gpu.matmul(gpu.upload(a), gpu.upload(b), c)
+    assert O.erro_rel(O.matmul(a, b), gpu.download(c)) < 1e-5
+
+
+SHAPES = [(1, 1, 1), (17, 33, 65), (64, 64, 64), (65, 64, 63), (130, 96, 80), (199, 130, 71), (256, 512, 128),
+          (300, 1030, 257), (2048, 10, 1024), (1024, 10, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_gemm_three_layouts(gpu, m, n, k):  # gpu.rs:244-295
+    a, b = sincos(m, k, n)
+    want = O.matmul(a, b)
+    ga, gb = gpu.upload(a), gpu.upload(b)
+    gat, gbt = gpu.upload(a.T.copy()), gpu.upload(b.T.copy())
+    c1, c2, c3 = gpu.zeros((m, n)), gpu.zeros((m, n)), gpu.zeros((m, n))
+    gpu.matmul(ga, gb, c1)
+    gpu.matmul_at_b(gat, gb, c2)
+    gpu.matmul_a_bt(ga, gbt, c3)
+    for name, c in (("mm", c1), ("mm_atb", c2), ("mm_abt", c3)):
+        e = O.erro_rel(want, gpu.download(c))
+        assert e < 1e-5, (name, m, n, k, e)
+
+
+def test_gemm_large_tile_path(gpu):
+    # 2048 x 2048 output takes the 128x128 tile kernel
+    m, n, k = 2048, 2048, 96
+    rng = np.random.default_rng(1)
+    a = rng.normal(size=(m, k)).astype(np.float32)
+    b = rng.normal(size=(k, n)).astype(np.float32)
+    want = O.matmul(a, b)
+    for layout, A, B in ((G.NN, a, b), (G.TN, a.T.copy(), b), (G.NT, a, b.T.copy())):
+        c = gpu.zeros((m, n))
+        gpu.gemm(layout, gpu.upload(A), gpu.upload(B), c)
+        assert O.erro_rel(want, gpu.download(c)) < 1e-5, layout
+
+
+def test_gemm_epilogues(gpu):
+    m, n, k = 130, 200, 77
+    rng = np.random.default_rng(2)
+    a = rng.normal(size=(m, k)).astype(np.float32)
+    w = rng.normal(size=(k, n)).astype(np.float32)
+    bias = rng.normal(size=(1, n)).astype(np.float32)
+    z = O.matmul(a, w) + bias
+    ga, gw, gbias = gpu.upload(a), gpu.upload(w), gpu.upload(bias)
+    c = gpu.zeros((m, n))
+    gpu.matmul_bias(ga, gw, c, gbias, relu=False)
+    assert O.erro_rel(z, gpu.download(c)) < 1e-5
+    gpu.matmul_bias(ga, gw, c, gbias, relu=True)
+    got = gpu.download(c)
+    assert O.erro_rel(np.maximum(z, 0), got) < 1e-5 and (got >= 0).all()
+    # δ_prev = (δ·Wᵀ) ⊙ 1[A > 0]: mask from a post-ReLU activation
+    d = rng.normal(size=(m, n)).astype(np.float32)
+    act = np.maximum(rng.normal(size=(m, k)).astype(np.float32), 0)
+    want = O.matmul(d, w.T.copy()) * (act > 0)
+    out = gpu.zeros((m, k))
+    gpu.matmul_a_bt(gpu.upload(d), gw, out, relu_mask_from=gpu.upload(act))
+    got = gpu.download(out)
+    assert O.erro_rel(want, got) < 1e-5
+    assert np.all(got[act <= 0] == 0)
+
+
+@pytest.mark.parametrize("k,m,n", [(2048, 1024, 10), (64, 130, 96), (513, 64, 1024)])
+def test_tn_gemm_fused_colsum(gpu, k, m, n):
+    rng = np.random.default_rng(3)
+    x = rng.normal(size=(k, m)).astype(np.float32)
+    d = rng.normal(size=(k, n)).astype(np.float32)
+    c, cs = gpu.zeros((m, n)), gpu.zeros((1, n))
+    gpu.matmul_at_b(gpu.upload(x), gpu.upload(d), c, colsum=cs)
+    assert O.erro_rel(O.matmul(x.T.copy(), d), gpu.download(c)) < 1e-5
+    assert O.erro_rel(O.reduce_to(d, (1, n)), gpu.download(cs)) < 1e-5
+    # integer-valued δ: every order gives the exact sum
+    di = rng.integers(-8, 9, size=(k, n)).astype(np.float32)
+    gpu.matmul_at_b(gpu.upload(x), gpu.upload(di), c, colsum=cs)
+    assert np.array_equal(gpu.download(cs).reshape(-1), di.sum(0, dtype=np.float64).astype(np.float32))
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 4096), (32, 96, 2048), (128, 64, 1024)])
+def test_split_k_against_whole_gemm(gpu, m, n, k):  # gpu.rs:383-430
+    a, b = sincos(m, k, n)
+    want = O.matmul(a, b)
+    ga, gat, gb = gpu.upload(a), gpu.upload(a.T.copy()), gpu.upload(b)
+    whole = gpu.zeros((m, n))
+    gpu.matmul(ga, gb, whole)
+    e_whole = O.erro_rel(want, gpu.download(whole))
+    whole_t = gpu.zeros((m, n))
+    gpu.matmul_at_b(gat, gb, whole_t)
+    for slices in (1, 2, 4, 8, 16):
+        for trans, inp, ref in ((False, ga, whole), (True, gat, whole_t)):
+            c = gpu.zeros((m, n))
+            part = gpu.zeros((slices * m + slices, n))
+            gpu.split_k(inp, gb, c, part, slices, trans)
+            got = gpu.download(c)
+            e = O.erro_rel(want, got)
+            assert e < max(3 * e_whole, 2e-5), (slices, trans, e, e_whole)
+            if slices == 1:
+                assert np.array_equal(got, gpu.download(ref))
+            c2 = gpu.zeros((m, n))
+            gpu.split_k(inp, gb, c2, part, slices, trans)
+            assert np.array_equal(got, gpu.download(c2))  # deterministic
+
+
+def test_split_k_fused_colsum(gpu):
+    rng = np.random.default_rng(4)
+    k, m, n, s = 4096, 100, 12, 8
+    x = rng.normal(size=(k, m)).astype(np.float32)
+    d = rng.normal(size=(k, n)).astype(np.float32)
+    c, cs = gpu.zeros((m, n)), gpu.zeros((1, n))
+    part = gpu.zeros((s * m * n + s * n,))
+    gpu.split_k(gpu.upload(x), gpu.upload(d), c, part, s, True, colsum=cs)
+    assert O.erro_rel(O.matmul(x.T.copy(), d), gpu.download(c)) < 1e-5
+    assert O.erro_rel(O.reduce_to(d, (1, n)), gpu.download(cs)) < 1e-5
+
+
+@pytest.mark.parametrize("rows,cols,dt", [(2048, 1024, G.F32), (33, 7, G.F32), (5000, 300, G.BF16),
+                                          (4096, 512, G.F16), (1, 1, G.F32)])
+def test_colsum(gpu, rows, cols, dt):
+    rng = np.random.default_rng(5)
+    x = rng.normal(size=(rows, cols)).astype(np.float32)
+    if dt == G.BF16:
+        x = G.bf16_bits_to_f32(G.f32_to_bf16_bits(x))
+    elif dt == G.F16:
+        x = x.astype(np.float16).astype(np.float32)
+    out = gpu.zeros((1, cols))
+    gpu.colsum(gpu.upload(x, dt), out)
+    assert O.erro_rel(O.reduce_to(x, (1, cols)), gpu.download(out)) < 1e-5
+
+
+def test_softmax_xent_matches_cpu_and_flags_bad_labels(gpu):
+    rng = np.random.default_rng(6)
+    B, C = 300, 10
+    z = (rng.normal(size=(B, C)) * 4).astype(np.float32)
+    lab = rng.integers(0, C, size=B).astype(np.uint32)
+    p = O.softmax_rows(z)
+    want_delta = ((p - O.one_hot(lab, C)) * np.float32(1.0 / B)).astype(np.float32)
+    want_loss = -np.log(np.maximum(p[np.arange(B), lab], np.float32(1e-12)))
+    gz, gl = gpu.upload(z), G.upload_labels(gpu, lab)
+    d, lr = gpu.zeros((B, C)), gpu.zeros((B,))
+    gpu.softmax_xent(gz, gl, d, lr)
+    assert O.erro_rel(want_delta, gpu.download(d)) < 1e-6
+    assert np.max(np.abs(want_loss - gpu.download(lr))) < 1e-5
+    gpu.sync()
+    lab[7] = C  # out of range: reported at the next blocking call, nothing read out of bounds
+    gpu.softmax_xent(gz, G.upload_labels(gpu, lab), d, lr)
+    with pytest.raises(G.RtError) as e:
+        gpu.sync()
+    assert e.value.status == "RT_ERR_LABEL"
+    gpu.sync()  # flag cleared once reported
+
+
+def test_relu_bias_add_relu_bwd(gpu):
+    rng = np.random.default_rng(7)
+    z = rng.normal(size=(77, 33)).astype(np.float32)
+    b = rng.normal(size=(1, 33)).astype(np.float32)
+    gz = gpu.upload(z)
+    gpu.bias_add(gz, gpu.upload(b))
+    assert np.array_equal(gpu.download(gz), (z + b).astype(np.float32))
+    y = gpu.zeros((77, 33))
+    gpu.relu(gz, y)
+    assert np.array_equal(gpu.download(y), np.maximum(z + b, 0))
+    d = rng.normal(size=(77, 33)).astype(np.float32)
+    gd = gpu.upload(d)
+    gpu.relu_bwd(y, gd)
+    assert np.array_equal(gpu.download(gd), np.where(np.maximum(z + b, 0) > 0, d, 0).astype(np.float32))
+
+
+def test_adam_and_sgd_are_bit_exact_with_cpu_arithmetic(gpu):
+    # Same inputs -> same bits as optim.rs's expression order.
+    rng = np.random.default_rng(8)
+    n = 10_001
+    theta = rng.normal(size=(1, n)).astype(np.float32)
+    p = O.Param(theta)
+    opt = O.Optimizer("adam", 1e-3)
+    gt, gm, gv = gpu.upload(theta), gpu.zeros((1, n)), gpu.zeros((1, n))
+    for t in range(1, 6):
+        g = rng.normal(size=(1, n)).astype(np.float32) * np.float32(10.0 ** -t)
+        tp = O.Tape()
+        tp.watch(p).mul(tp.constant(g)).sum().backward()
+        opt.step([p], tp)
+        gpu.adam(gt, gm, gv, gpu.upload(g), 1e-3, (0.9, 0.999), t)
+        assert np.array_equal(gpu.download(gt), p.value()), t
+    p2 = O.Param(theta)
+    sgd = O.Optimizer("sgd", 0.01, 0.9)
+    gt2, vel = gpu.upload(theta), gpu.zeros((1, n))
+    for _ in range(3):
+        g = rng.normal(size=(1, n)).astype(np.float32)
+        tp = O.Tape()
+        tp.watch(p2).mul(tp.constant(g)).sum().backward()
+        sgd.step([p2], tp)
+        gpu.sgd(gt2, gpu.upload(g), 0.01, 0.9, vel)
+    assert np.array_equal(gpu.download(gt2), p2.value())
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 64, 64), (256, 128, 512), (512, 512, 256), (130, 70, 200)])
+@pytest.mark.parametrize("dt", [G.F16, G.BF16])
+def test_half_gemm_three_layouts(gpu, m, n, k, dt):  # gpu.rs:445-503
+    a = np.sin(np.arange(m * k, dtype=np.float32) * np.float32(0.019)).astype(np.float32).reshape(m, k)
+    b = np.cos(np.arange(k * n, dtype=np.float32) * np.float32(0.013)).astype(np.float32).reshape(k, n)
+    want = O.matmul(a, b)
+    if dt == G.F16:
+        ar, br = a.astype(np.float16).astype(np.float32), b.astype(np.float16).astype(np.float32)
+        bound = 10 * np.sqrt(k) * 2.0 ** -11
+    else:
+        ar, br = G.bf16_bits_to_f32(G.f32_to_bf16_bits(a)), G.bf16_bits_to_f32(G.f32_to_bf16_bits(b))
+        bound = 10 * np.sqrt(k) * 2.0 ** -8
+    exact_inputs = O.matmul(ar, br)  # same rounded operands, f32 accumulate
+    for layout, A, B in ((G.NN, a, b), (G.TN, a.T.copy(), b), (G.NT, a, b.T.copy())):
+        c = gpu.zeros((m, n))
+        gpu.gemm(layout, gpu.upload(A, dt), gpu.upload(B, dt), c)
+        got = gpu.download(c)
+        assert O.erro_rel(want, got) < bound, (layout, O.erro_rel(want, got), bound)
+        assert O.erro_rel(exact_inputs, got) < 1e-5, (layout, O.erro_rel(exact_inputs, got))
+
+
+def test_half_gemm_bf16_output_and_epilogue(gpu):
+    rng = np.random.default_rng(9)
+    m, n, k = 256, 384, 192
+    a = G.bf16_bits_to_f32(G.f32_to_bf16_bits(rng.normal(size=(m, k)).astype(np.float32)))
+    w = G.bf16_bits_to_f32(G.f32_to_bf16_bits(rng.normal(size=(k, n)).astype(np.float32)))
+    bias = rng.normal(size=(1, n)).astype(np.float32)
+    want = np.maximum(O.matmul(a, w) + bias, 0)
+    c = gpu.zeros((m, n), G.BF16)
+    gpu.gemm(G.NN, gpu.upload(a, G.BF16), gpu.upload(w, G.BF16), c, G.EPI_BIAS_RELU, gpu.upload(bias))
+    got = G.bf16_bits_to_f32(gpu.download(c))
+    assert np.max(np.abs(got - want) / (1 + np.abs(want))) < 2.0 ** -8
+
+
+def test_convert_round_trip(gpu):
+    x = np.random.default_rng(10).normal(size=(1000,)).astype(np.float32)
+    x[:4] = [1.00390625, 1.01171875, 6.0e-8, -65504.0]
+    src = gpu.upload(x)
+    hb, hf = gpu.zeros((1000,), G.BF16), gpu.zeros((1000,), G.F16)
+    gpu.convert(src, hb)
+    gpu.convert(src, hf)
+    assert np.array_equal(gpu.download(hb), G.f32_to_bf16_bits(x))
+    assert np.array_equal(gpu.download(hf), x.astype(np.float16))  # RNE, subnormals kept
+
+
+def test_shape_errors_are_reported(gpu):
+    a, b, c = gpu.zeros((4, 5)), gpu.zeros((6, 7)), gpu.zeros((4, 7))
+    with pytest.raises(G.RtError) as e:
+        gpu.matmul(a, b, c)
+    assert e.value.status == "RT_ERR_SHAPE"
+    with pytest.raises(G.RtError) as e:
+        gpu.matmul(gpu.zeros((4, 6)), b, gpu.zeros((4, 8)))
+    assert e.value.status == "RT_ERR_SHAPE"
