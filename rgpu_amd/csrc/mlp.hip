@@ -147,6 +147,14 @@ static int run_forward(rt_mlp* p, const rt_buf* x) {
   return RT_OK;
 }
 
+namespace rt {
+void mlp_release(rt_mlp* p) {
+  hipStreamSynchronize(p->ctx->stream);
+  hipFree(p->arena);
+  delete p;
+}
+}  // namespace rt
+
 extern "C" {
 
 int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* const* weights, const float* const* biases,
@@ -269,15 +277,16 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   n += 1;  // optimizer
   if (p->mixed) n += 2;  // overflow flag reset + non-finite check
   p->dispatches = n;
+  c->mlps.push_back(p);
   *out = p;
   return RT_OK;
 }
 
 int rt_mlp_destroy(rt_mlp* p) {
   if (p == nullptr) return RT_OK;
-  hipStreamSynchronize(p->ctx->stream);
-  hipFree(p->arena);
-  delete p;
+  auto& v = p->ctx->mlps;
+  v.erase(std::remove(v.begin(), v.end(), p), v.end());
+  mlp_release(p);
   return RT_OK;
 }
 

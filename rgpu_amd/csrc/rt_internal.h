@@ -38,12 +38,16 @@ struct rt_ctx {
   float* scratch = nullptr;
   size_t scratch_elems = 0;
   bool profiling = false;
+  // Children freed by rt_close if the caller has not freed them.
+  std::vector<rt_buf*> bufs;
+  std::vector<rt_mlp*> mlps;
   std::vector<rt_prof_rec> prof;
   std::vector<hipEvent_t> event_pool;
 };
 
 namespace rt {
 
+void mlp_release(rt_mlp* p);  // frees the plan's device memory and the struct
 size_t dtype_size(rt_dtype d);
 int fail(rt_ctx* c, int code, const char* fmt, ...);
 int hip_fail(rt_ctx* c, hipError_t e, const char* what);

@@ -147,6 +147,15 @@ int rt_close(rt_ctx* c) {
   CHECK_CTX(c);
   hipSetDevice(c->device);
   hipStreamSynchronize(c->stream);
+  // The context owns what was created on it: models and buffers the caller
+  // did not free go with it (their handles become invalid).
+  for (rt_mlp* p : c->mlps) mlp_release(p);
+  c->mlps.clear();
+  for (rt_buf* b : c->bufs) {
+    if (b->ptr) hipFree(b->ptr);
+    delete b;
+  }
+  c->bufs.clear();
   for (auto& r : c->prof) {
     hipEventDestroy(r.e0);
     hipEventDestroy(r.e1);
@@ -204,8 +213,14 @@ static int make_buf(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt
       return hip_fail(c, e, "hipMalloc");
     }
   }
+  c->bufs.push_back(b);
   *out = b;
   return RT_OK;
+}
+
+static void forget_buf(rt_ctx* c, rt_buf* b) {
+  auto it = std::find(c->bufs.begin(), c->bufs.end(), b);
+  if (it != c->bufs.end()) c->bufs.erase(it);
 }
 
 int rt_zeros(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out) {
@@ -219,6 +234,7 @@ int rt_zeros(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** 
     hipError_t e = fill_i32_launch(c->stream, static_cast<int*>(b->ptr), 0, words);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
+      forget_buf(c, b);
       hipFree(b->ptr);
       delete b;
       *out = nullptr;
@@ -235,6 +251,7 @@ int rt_upload(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, const vo
   rt_buf* b = *out;
   if (b->bytes > 0) {
     if (host == nullptr) {
+      forget_buf(c, b);
       hipFree(b->ptr);
       delete b;
       *out = nullptr;
@@ -243,6 +260,7 @@ int rt_upload(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, const vo
     hipError_t e = hipMemcpyAsync(b->ptr, host, b->bytes, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
+      forget_buf(c, b);
       hipFree(b->ptr);
       delete b;
       *out = nullptr;
@@ -276,6 +294,9 @@ int rt_write(rt_ctx* c, rt_buf* b, const void* host, size_t bytes) {
 int rt_free(rt_ctx* c, rt_buf* b) {
   CHECK_CTX(c);
   if (b == nullptr) return RT_OK;
+  if (std::find(c->bufs.begin(), c->bufs.end(), b) == c->bufs.end())
+    return fail(c, RT_ERR_INVALID, "buffer does not belong to this context");
+  forget_buf(c, b);
   // Work already enqueued may still read the buffer.
   hipStreamSynchronize(c->stream);
   if (b->ptr) hipFree(b->ptr);

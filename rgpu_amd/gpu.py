@@ -367,9 +367,10 @@ class GpuMlp:
         return cls(gpu, h.value, dims, lote)
 
     def destroy(self):
-        if self._h:
+        # A closed Gpu already released its models.
+        if self._h and self.gpu._h:
             lib().rt_mlp_destroy(self._h)
-            self._h = None
+        self._h = None
 
     def __del__(self):
         try:

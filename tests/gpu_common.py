@@ -46,3 +46,41 @@ def normal_batch(seed, rows, cols):
 
 def uniform_labels(seed, rows, classes):
     return O.Rng(seed).belows(rows, classes)
+
+
+def numpy_f32_trajectory(params, batches, lr, beta1=0.9, beta2=0.999, eps=1e-8):
+    """The same training step written directly in float32 numpy (BLAS GEMM
+    order, pairwise sums): an independent f32 implementation whose distance
+    from the oracle measures how much the trajectory moves under a change of
+    summation order alone.  Returns final params and per-step losses."""
+    Ws = [p.astype(np.float32).copy() for p in params[0::2]]
+    bs = [p.astype(np.float32).reshape(1, -1).copy() for p in params[1::2]]
+    ps = [a for pair in zip(Ws, bs) for a in pair]
+    m = [np.zeros_like(p) for p in ps]
+    v = [np.zeros_like(p) for p in ps]
+    f = np.float32
+    losses = []
+    for t, (x, lab) in enumerate(batches, start=1):
+        acts = [x.astype(np.float32)]
+        for l in range(len(Ws)):
+            z = acts[-1] @ Ws[l] + bs[l]
+            acts.append(np.maximum(z, f(0)) if l < len(Ws) - 1 else z)
+        z = acts[-1]
+        e = np.exp(z - z.max(1, keepdims=True))
+        p = e / e.sum(1, keepdims=True)
+        B = z.shape[0]
+        losses.append(float(-np.log(np.maximum(p[np.arange(B), lab], f(1e-12))).astype(np.float64).mean()))
+        delta = ((p - np.eye(z.shape[1], dtype=np.float32)[lab]) * f(1.0 / B)).astype(np.float32)
+        grads = [None] * len(ps)
+        for l in reversed(range(len(Ws))):
+            grads[2 * l] = acts[l].T @ delta
+            grads[2 * l + 1] = delta.sum(0, keepdims=True)
+            if l > 0:
+                delta = (delta @ Ws[l].T) * (acts[l] > 0)
+        c1 = f(1) - f(beta1) ** t
+        c2 = f(1) - f(beta2) ** t
+        for i, g in enumerate(grads):
+            m[i] = m[i] * f(beta1) + g * (f(1) - f(beta1))
+            v[i] = v[i] * f(beta2) + (g * g) * (f(1) - f(beta2))
+            ps[i] -= ((m[i] * (f(1) / c1)) / (np.sqrt(v[i] * (f(1) / c2)) + f(eps))) * f(lr)
+    return ps, losses
