@@ -5,21 +5,34 @@
 // mista.rs:58-323) -- half operands, f32 accumulate, the three layouts of the
 // backward pass -- rebuilt for gfx950 matrix cores and extended to bf16.
 //
-// Block = 256 threads = 4 wave64s (2x2), block tile 128x128, K staged 64 at a
-// time through LDS, double-buffered with register staging.  Both operand
-// tiles live in LDS k-contiguous, [row][64 + 8 pad] halves, so every MFMA
-// operand is one ds_read_b128 (8 consecutive k of one row; lane 16g+r reads
-// row r, k = 8g..8g+7).  The 72-half (36-dword) row stride puts the 16 rows
-// read by a lane group on distinct 4-bank groups.
+// Tiling.  Block = WGM x WGN wave64s, block tile BM x BN, K staged BK = 32 at
+// a time through LDS, double-buffered with register staging (one barrier per
+// K step).  Each wave owns (BM/WGM) x (BN/WGN) = TM x TN MFMA 16x16 tiles.
+// Large problems use 128x256 blocks of 8 waves: two waves per SIMD hide each
+// other's LDS and barrier latency (measured faster than 256x256 with one wave
+// of 128x128 per SIMD, which holds 256 accumulators per lane in AGPRs).
 //
-// Operands stored K-contiguous (A of NN/NT, B of NT) are copied 8 halves per
-// b128.  Operands stored M/N-contiguous (A of TN, B of NN/TN) are transposed
-// on the way into LDS: each thread loads a 4(k) x 8(m) block as four b128 rows
-// and writes eight 4-half k-runs (ds_write_b64), one per m.  For TN with a
-// colsum target, the blocks of the first M tile sum their LDS B tile rows
-// over k: db = 1ᵀ·δ in f32 with no extra HBM pass.
+// Operands are copied into LDS exactly as they are stored (b128 copies, no
+// transposition): K-contiguous operands as [row][BK+8], M/N-contiguous ones as
+// [k][cols+16].  An MFMA 16x16x32 operand is 8 halves per lane; lane 16g+r
+// takes row/col r and the k values {4g..4g+3} U {16+4g..16+4g+3} of the
+// 32-wide step (any k permutation is exact as long as A and B agree), read as
+// two 4-half pieces:
+//   * K-contiguous tile: ds_read_b64 of [row r][16h + 4g .. +3];
+//   * M/N-contiguous tile: ds_read_b64_tr_b16.  Within each 16-lane group,
+//     destination lane d = 4a+e receives element e of the 8-byte chunks read
+//     by source lanes a, a+4, a+8, a+12; so when source lane s reads
+//     [k = 16h + 4g + s/4][c0 + 4(s%4) .. +3], lane d receives the four k of
+//     column c0 + d.
+// With these k sets, the lanes of one half-wave read 8 consecutive k rows of
+// an M/N-contiguous tile whose row stride is 8 banks apart: conflict-free.
+//
+// For TN with a colsum target, the blocks of the first M tile also sum their
+// LDS B tiles over k (db = 1ᵀ·δ in f32, no extra HBM pass).  Split-K slices
+// write f32 partial planes reduced in slice order by splitk_reduce.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "rt_internal.h"
 
@@ -28,12 +41,13 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kThreads = 256;
-constexpr int BM = 128, BN = 128, BK = 64, KPAD = 8;
-constexpr int ROW = BK + KPAD;  // halves per LDS row
+constexpr int BK = 32;
+constexpr int KPAD = 8;   // K-contiguous rows: 40 halves = 20 dwords
+constexpr int MPAD = 16;  // M/N-contiguous rows: cols + 16 halves
 
 struct HalfArgs {
   const unsigned short* A;
@@ -67,10 +81,10 @@ __device__ inline float half_to_f32(unsigned short h) {
   else return (float)__builtin_bit_cast(_Float16, h);
 }
 
-// 8 consecutive halves (one b128) of a row-major matrix; zero outside.
-__device__ inline u4 load8(const unsigned short* base, int ld, int row, int col, int rows, int cols, int vec) {
+// 8 consecutive halves of a row-major matrix at (row, col); zero outside.
+__device__ inline u4 load8(const unsigned short* base, int ld, int row, int col, int rows, int cols, bool fast) {
   const unsigned short* src = base + (long long)row * ld + col;
-  if (vec && row < rows && col + 7 < cols) return *reinterpret_cast<const u4*>(src);
+  if (fast) return *reinterpret_cast<const u4*>(src);
   unsigned short h[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) h[e] = (row < rows && col + e < cols) ? src[e] : (unsigned short)0;
@@ -80,62 +94,94 @@ __device__ inline u4 load8(const unsigned short* base, int ld, int row, int col,
   return v;
 }
 
-// Staged global data of one operand tile for one thread (4 x b128).
-struct Stage {
-  u4 v[4];
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
+// where the body indexes the accumulator array, which must stay in registers.
+template <int B, int E, class F>
+__device__ inline void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+__device__ inline u2 lds_tr(const unsigned short* p) {
+  s4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)(p));
+  return __builtin_bit_cast(u2, r);
+}
+
+// One operand of the block: tile geometry and its global <-> LDS movement.
+// ROWS = BM (A) or BN (B); KC = stored K-contiguous.
+template <int ROWS, bool KC, int THREADS>
+struct Operand {
+  static constexpr int STRIDE = KC ? (BK + KPAD) : (ROWS + MPAD);  // halves per LDS row
+  static constexpr int ELEMS = KC ? ROWS * STRIDE : BK * STRIDE;
+  static constexpr int CHUNKS = ROWS * BK / 8;  // b128 per tile
+  static constexpr int PER_THREAD = CHUNKS / THREADS;
+  static_assert(CHUNKS % THREADS == 0, "tile must split evenly over threads");
+
+  u4 v[PER_THREAD];
+
+  // Global (rows r0.., k0..) -> registers.
+  __device__ inline void load(const unsigned short* base, int ld, int r0, int k0, int rows, int ke, bool full,
+                              int tid) {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int idx = tid + THREADS * i;
+      if constexpr (KC) {
+        const int row = idx / (BK / 8), kc = idx % (BK / 8);
+        v[i] = load8(base, ld, r0 + row, k0 + 8 * kc, rows, ke, full);
+      } else {
+        const int kk = idx / (ROWS / 8), c = idx % (ROWS / 8);
+        v[i] = load8(base, ld, k0 + kk, r0 + 8 * c, ke, rows, full);
+      }
+    }
+  }
+  __device__ inline void store(unsigned short* lds, int tid) const {
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+      const int idx = tid + THREADS * i;
+      if constexpr (KC) {
+        *reinterpret_cast<u4*>(&lds[(idx / (BK / 8)) * STRIDE + 8 * (idx % (BK / 8))]) = v[i];
+      } else {
+        *reinterpret_cast<u4*>(&lds[(idx / (ROWS / 8)) * STRIDE + 8 * (idx % (ROWS / 8))]) = v[i];
+      }
+    }
+  }
+  // MFMA operand (8 halves) of the 16 rows [rbase, rbase+16) for lane (g, r).
+  __device__ inline u4 frag(const unsigned short* lds, int rbase, int g, int r) const {
+    u2 lo, hi;
+    if constexpr (KC) {
+      const unsigned short* p = &lds[(rbase + r) * STRIDE + 4 * g];
+      lo = *reinterpret_cast<const u2*>(p);
+      hi = *reinterpret_cast<const u2*>(p + 16);
+    } else {
+      const unsigned short* p = &lds[(4 * g + (r >> 2)) * STRIDE + rbase + 4 * (r & 3)];
+      lo = lds_tr(p);
+      hi = lds_tr(p + 16 * STRIDE);
+    }
+    return u4{lo[0], lo[1], hi[0], hi[1]};
+  }
 };
 
-// K-contiguous operand ([rows][K]): 128 rows x 64 k = 1024 b128, 4 per thread.
-__device__ inline void load_kc(Stage& st, const unsigned short* base, int ld, int r0, int k0, int rows, int ke, int vec,
-                               int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = tid + kThreads * i;
-    st.v[i] = load8(base, ld, r0 + (idx >> 3), k0 + 8 * (idx & 7), rows, ke, vec);
-  }
-}
-__device__ inline void store_kc(const Stage& st, unsigned short* lds, int tid) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int idx = tid + kThreads * i;
-    *reinterpret_cast<u4*>(&lds[(idx >> 3) * ROW + 8 * (idx & 7)]) = st.v[i];
-  }
-}
-
-// M/N-contiguous operand ([K][rows]): thread owns k rows 4kq..4kq+3 and
-// columns 8mq..8mq+7 of the 64 x 128 tile.
-__device__ inline void load_mc(Stage& st, const unsigned short* base, int ld, int r0, int k0, int rows, int ke, int vec,
-                               int tid) {
-  const int kq = tid >> 4, mq = tid & 15;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) st.v[j] = load8(base, ld, k0 + 4 * kq + j, r0 + 8 * mq, ke, rows, vec);
-}
-__device__ inline void store_mc(const Stage& st, unsigned short* lds, int tid) {
-  const int kq = tid >> 4, mq = tid & 15;
-#pragma unroll
-  for (int mi = 0; mi < 8; ++mi) {
-    const int d = mi >> 1;
-    const int sh = (mi & 1) * 16;
-    const unsigned int h0 = (st.v[0][d] >> sh) & 0xffffu, h1 = (st.v[1][d] >> sh) & 0xffffu;
-    const unsigned int h2 = (st.v[2][d] >> sh) & 0xffffu, h3 = (st.v[3][d] >> sh) & 0xffffu;
-    u2 w;
-    w[0] = h0 | (h1 << 16);
-    w[1] = h2 | (h3 << 16);
-    *reinterpret_cast<u2*>(&lds[(8 * mq + mi) * ROW + 4 * kq]) = w;
-  }
-}
-
-template <bool A_KC, bool B_KC, bool IS_BF16>
-__global__ __launch_bounds__(kThreads) void gemm_half_kernel(HalfArgs p) {
-  __shared__ __attribute__((aligned(16))) unsigned short sA[2][BM * ROW];
-  __shared__ __attribute__((aligned(16))) unsigned short sB[2][BN * ROW];
+template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC, bool IS_BF16>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_kernel(HalfArgs p) {
+  constexpr int THREADS = 64 * WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;  // wave tile
+  constexpr int TM = WM / 16, TN = WN / 16;
+  using OpA = Operand<BM, A_KC, THREADS>;
+  using OpB = Operand<BN, B_KC, THREADS>;
+  // One LDS buffer: A tiles (2 stages), then B tiles (2 stages); the
+  // epilogue reuses all of it for staging.
+  __shared__ __attribute__((aligned(16))) unsigned short smem[2 * OpA::ELEMS + 2 * OpB::ELEMS];
+  auto sA = [&](int buf) { return smem + buf * OpA::ELEMS; };
+  auto sB = [&](int buf) { return smem + 2 * OpA::ELEMS + buf * OpB::ELEMS; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r = lane & 15;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
 
-  // XCD-contiguous renumbering + grouped raster (as in the f32 kernel).
+  // XCD-contiguous renumbering + grouped raster (GROUP M tiles per band).
   int bid = blockIdx.x;
   const int nb = gridDim.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
@@ -152,57 +198,51 @@ __global__ __launch_bounds__(kThreads) void gemm_half_kernel(HalfArgs p) {
   const int kb = blockIdx.z * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
+  const bool rows_in = (m0 + BM <= p.M) && (n0 + BN <= p.N);
 
-  Stage sa, sb;
+  OpA oa;
+  OpB ob;
   auto load_tiles = [&](int k0) {
-    if constexpr (A_KC) load_kc(sa, p.A, p.lda, m0, k0, p.M, ke, p.vec_a, tid);
-    else load_mc(sa, p.A, p.lda, m0, k0, p.M, ke, p.vec_a, tid);
-    if constexpr (B_KC) load_kc(sb, p.B, p.ldb, n0, k0, p.N, ke, p.vec_b, tid);
-    else load_mc(sb, p.B, p.ldb, n0, k0, p.N, ke, p.vec_b, tid);
-  };
-  auto store_tiles = [&](int buf) {
-    if constexpr (A_KC) store_kc(sa, sA[buf], tid);
-    else store_mc(sa, sA[buf], tid);
-    if constexpr (B_KC) store_kc(sb, sB[buf], tid);
-    else store_mc(sb, sB[buf], tid);
+    const bool full = rows_in && (k0 + BK <= ke);
+    oa.load(p.A, p.lda, m0, k0, p.M, ke, full && p.vec_a, tid);
+    ob.load(p.B, p.ldb, n0, k0, p.N, ke, full && p.vec_b, tid);
   };
 
-  f4 acc[4][4];
+  f4 acc[TM][TN];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < TM; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = 0; u < TN; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](int buf) {
-    const unsigned short* as = sA[buf];
-    const unsigned short* bs = sB[buf];
+    u4 bf[TN];
 #pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      u4 af[4], bf[4];
+    for (int u = 0; u < TN; ++u) bf[u] = ob.frag(sB(buf), wn + 16 * u, g, r);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) af[t] = *reinterpret_cast<const u4*>(&as[(wm + 16 * t + r) * ROW + 32 * kk + 8 * g]);
+    for (int t = 0; t < TM; ++t) {
+      const u4 af = oa.frag(sA(buf), wm + 16 * t, g, r);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) bf[u] = *reinterpret_cast<const u4*>(&bs[(wn + 16 * u + r) * ROW + 32 * kk + 8 * g]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if constexpr (IS_BF16)
-            acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[t]),
-                                                                __builtin_bit_cast(bf16x8, bf[u]), acc[t][u], 0, 0, 0);
-          else
-            acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af[t]),
-                                                               __builtin_bit_cast(f16x8, bf[u]), acc[t][u], 0, 0, 0);
-        }
+      for (int u = 0; u < TN; ++u) {
+        if constexpr (IS_BF16)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af),
+                                                              __builtin_bit_cast(bf16x8, bf[u]), acc[t][u], 0, 0, 0);
+        else
+          acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af),
+                                                             __builtin_bit_cast(f16x8, bf[u]), acc[t][u], 0, 0, 0);
+      }
     }
   };
 
-  const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0 && tid < BN;
-  float cs = 0.0f;
+  // Column sums of B over k (the bias gradient when B = δ), first M tile only.
+  const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0;
+  float cs[(BN + THREADS - 1) / THREADS];
+#pragma unroll
+  for (int i = 0; i < (BN + THREADS - 1) / THREADS; ++i) cs[i] = 0.0f;
 
   if (nk > 0) {
     load_tiles(kb);
-    store_tiles(0);
+    oa.store(sA(0), tid);
+    ob.store(sB(0), tid);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       const int cur = kt & 1;
@@ -210,61 +250,126 @@ __global__ __launch_bounds__(kThreads) void gemm_half_kernel(HalfArgs p) {
       compute(cur);
       if constexpr (!B_KC) {
         if (do_cs) {
-          const unsigned short* row = &sB[cur][tid * ROW];
+#pragma unroll
+          for (int i = 0; i < (BN + THREADS - 1) / THREADS; ++i) {
+            const int col = tid + THREADS * i;
+            if (col < BN) {
+              const unsigned short* colp = &sB(cur)[col];
 #pragma unroll 8
-          for (int k = 0; k < BK; ++k) cs += half_to_f32<IS_BF16>(row[k]);
+              for (int k = 0; k < BK; ++k) cs[i] += half_to_f32<IS_BF16>(colp[k * OpB::STRIDE]);
+            }
+          }
         }
       }
-      if (kt + 1 < nk) store_tiles(cur ^ 1);
+      if (kt + 1 < nk) {
+        oa.store(sA(cur ^ 1), tid);
+        ob.store(sB(cur ^ 1), tid);
+      }
       __syncthreads();
     }
   }
 
-  if (do_cs && n0 + tid < p.N) p.colsum[(long long)blockIdx.z * p.N + n0 + tid] = cs;
-
-  // Epilogue: acc[t][u][q] is C(m0+wm+16t+4g+q, n0+wn+16u+r).
-  const bool partial = gridDim.z > 1;
-  const bool out_bf16 = !partial && p.out_bf16;
+  if (do_cs) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int col = n0 + wn + 16 * u + r;
-    if (col >= p.N) continue;
-    const float bv = (!partial && p.bias != nullptr) ? p.bias[col] : 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = m0 + wm + 16 * t + 4 * g + q;
-        if (row >= p.M) continue;
-        float v = acc[t][u][q];
-        const long long off = (long long)row * p.ldc + col;
-        if (!partial) {
-          if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
-            v = v + bv;
-            if (p.epi == RT_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
-          } else if (p.epi == RT_EPI_RELU_MASK) {
-            const float mv = p.mask_bf16 ? bf16_to_f32(static_cast<const unsigned short*>(p.mask)[off])
-                                         : static_cast<const float*>(p.mask)[off];
-            if (!(mv > 0.0f)) v = 0.0f;
-          }
-        }
-        if (out_bf16) static_cast<unsigned short*>(p.C)[off] = f32_to_bf16_rne(v);
-        else static_cast<float*>(p.C)[off + (long long)blockIdx.z * p.split_stride] = v;
-      }
+    for (int i = 0; i < (BN + THREADS - 1) / THREADS; ++i) {
+      const int col = tid + THREADS * i;
+      if (col < BN && n0 + col < p.N) p.colsum[(long long)blockIdx.z * p.N + n0 + col] = cs[i];
     }
   }
+
+  // Epilogue through LDS, one 16-row slab of the wave tile at a time: the
+  // accumulators acc[t][u][q] = C(m0+wm+16t+4g+q, n0+wn+16u+r) are parked in
+  // a per-wave [16][WN+4] f32 region, then each lane reads 4 consecutive
+  // columns back, applies bias / ReLU / mask and stores 16 (f32) or 8 (bf16)
+  // bytes.  Bounded register use and coalesced stores.
+  constexpr int SROW = WN + 4;
+  static_assert(16 * SROW * 4 * WGM * WGN <= (int)sizeof(smem), "epilogue staging must fit in LDS");
+  float* stage = reinterpret_cast<float*>(smem) + wave * 16 * SROW;
+  const bool partial = gridDim.z > 1;
+  const bool out_bf16 = !partial && p.out_bf16;
+  const bool vec_c = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+  float* Cf = static_cast<float*>(p.C) + (partial ? (long long)blockIdx.z * p.split_stride : 0);
+  unsigned short* Ch = static_cast<unsigned short*>(p.C);
+  __syncthreads();  // main-loop LDS reads are finished
+  static_for<0, TM>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+#pragma unroll
+    for (int u = 0; u < TN; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) stage[(4 * g + q) * SROW + 16 * u + r] = acc[t][u][q];
+    __syncthreads();
+    constexpr int C4 = WN / 4;  // float4 columns per slab row
+#pragma unroll
+    for (int j = 0; j < 16 * C4 / 64; ++j) {
+      const int idx = lane + 64 * j;
+      const int rr = idx / C4, c4 = idx % C4;
+      const int row = m0 + wm + 16 * t + rr;
+      const int col = n0 + wn + 4 * c4;
+      if (row >= p.M || col >= p.N) continue;
+      f4 v = *reinterpret_cast<const f4*>(&stage[rr * SROW + 4 * c4]);
+      const long long off = (long long)row * p.ldc + col;
+      const int nv = min(4, p.N - col);
+      if (!partial) {
+        if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (e < nv) v[e] = v[e] + p.bias[col + e];
+            if (p.epi == RT_EPI_BIAS_RELU) v[e] = fmaxf(v[e], 0.0f);
+          }
+        } else if (p.epi == RT_EPI_RELU_MASK) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (e < nv) {
+              const float mv = p.mask_bf16 ? bf16_to_f32(static_cast<const unsigned short*>(p.mask)[off + e])
+                                           : static_cast<const float*>(p.mask)[off + e];
+              if (!(mv > 0.0f)) v[e] = 0.0f;
+            }
+          }
+        }
+      }
+      if (out_bf16) {
+        if (vec_c && nv == 4) {
+          u2 w;
+          w[0] = (unsigned)f32_to_bf16_rne(v[0]) | ((unsigned)f32_to_bf16_rne(v[1]) << 16);
+          w[1] = (unsigned)f32_to_bf16_rne(v[2]) | ((unsigned)f32_to_bf16_rne(v[3]) << 16);
+          *reinterpret_cast<u2*>(&Ch[off]) = w;
+        } else {
+          for (int e = 0; e < nv; ++e) Ch[off + e] = f32_to_bf16_rne(v[e]);
+        }
+      } else {
+        if (vec_c && nv == 4) *reinterpret_cast<f4*>(&Cf[off]) = v;
+        else
+          for (int e = 0; e < nv; ++e) Cf[off + e] = v[e];
+      }
+    }
+    __syncthreads();
+  });
+}
+
+template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
+hipError_t launch_cfg(hipStream_t s, HalfArgs a, int splits, bool bf16) {
+  a.tiles_m = (a.M + BM - 1) / BM;
+  a.tiles_n = (a.N + BN - 1) / BN;
+  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+  dim3 block(64 * WGM * WGN);
+  if (bf16)
+    hipLaunchKernelGGL((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false>), grid, block, 0, s, a);
+  return hipGetLastError();
 }
 
 template <bool A_KC, bool B_KC>
 hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16) {
-  a.tiles_m = (a.M + BM - 1) / BM;
-  a.tiles_n = (a.N + BN - 1) / BN;
-  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
-  if (bf16)
-    hipLaunchKernelGGL((gemm_half_kernel<A_KC, B_KC, true>), grid, dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((gemm_half_kernel<A_KC, B_KC, false>), grid, dim3(kThreads), 0, s, a);
-  return hipGetLastError();
+  // 128x256 blocks of 8 waves (2 per SIMD, 64x64 wave tiles) once they give
+  // at least one block per CU -- the fastest of the measured shapes for all
+  // three layouts at 8192x4096x4096; 128x128 (4 waves) for mid sizes; 64x64
+  // for small ones.
+  const long long tbig = (long long)((a.M + 127) / 128) * ((a.N + 255) / 256) * splits;
+  const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
+  if (tbig >= 256) return launch_cfg<128, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16);
+  if (t128 >= 128) return launch_cfg<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+  return launch_cfg<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
 }
 
 }  // namespace

@@ -321,3 +321,36 @@ def test_shape_errors_are_reported(gpu):
     with pytest.raises(G.RtError) as e:
         gpu.matmul(gpu.zeros((4, 6)), b, gpu.zeros((4, 8)))
     assert e.value.status == "RT_ERR_SHAPE"
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (4100, 4000, 96)])
+@pytest.mark.parametrize("dt", [G.BF16, G.F16])
+def test_half_gemm_large_tiles(gpu, m, n, k, dt):
+    # Shapes big enough for the 256x256 block configuration, including ragged
+    # edge tiles; against the float64 product of the same rounded operands.
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((m, k), dtype=np.float32)
+    b = rng.standard_normal((k, n), dtype=np.float32)
+    if dt == G.F16:
+        ar, br = a.astype(np.float16).astype(np.float64), b.astype(np.float16).astype(np.float64)
+    else:
+        ar = G.bf16_bits_to_f32(G.f32_to_bf16_bits(a)).astype(np.float64)
+        br = G.bf16_bits_to_f32(G.f32_to_bf16_bits(b)).astype(np.float64)
+    exact = ar @ br
+    bias = rng.standard_normal((1, n), dtype=np.float32)
+    for layout, A, B in ((G.NN, a, b), (G.TN, a.T.copy(), b), (G.NT, a, b.T.copy())):
+        ga, gb = gpu.upload(A, dt), gpu.upload(B, dt)
+        c = gpu.zeros((m, n))
+        gpu.gemm(layout, ga, gb, c)
+        e = O.erro_rel(exact, gpu.download(c))
+        print(f"layout {layout} {m}x{n}x{k}: erro_rel vs exact {e:.2e}")
+        assert e < 2e-6 * np.sqrt(k), (layout, e)
+    # bf16 output with the bias+ReLU epilogue, and TN with the fused colsum
+    cb = gpu.zeros((m, n), G.BF16)
+    gpu.gemm(G.NN, gpu.upload(a, dt), gpu.upload(b, dt), cb, G.EPI_BIAS_RELU, gpu.upload(bias))
+    want = np.maximum(exact + bias, 0)
+    got = G.bf16_bits_to_f32(gpu.download(cb))
+    assert np.max(np.abs(got - want) / (1 + np.abs(want))) < 2.0 ** -8
+    cs = gpu.zeros((1, n))
+    gpu.gemm(G.TN, gpu.upload(a.T.copy(), dt), gpu.upload(b, dt), c, colsum=cs)
+    assert O.erro_rel(br.sum(0, keepdims=True), gpu.download(cs)) < 1e-5
