@@ -5,27 +5,26 @@
 // mista.rs:58-323) -- half operands, f32 accumulate, the three layouts of the
 // backward pass -- rebuilt for gfx950 matrix cores and extended to bf16.
 //
-// Tiling.  Block = WGM x WGN wave64s, block tile BM x BN, K staged BK = 32 at
+// Tiling.  Block = WGM x WGN wave64s, block tile BM x BN, K staged BK = 64 at
 // a time through LDS, double-buffered with register staging (one barrier per
 // K step).  Each wave owns (BM/WGM) x (BN/WGN) = TM x TN MFMA 16x16 tiles.
-// Large problems use 128x256 blocks of 8 waves: two waves per SIMD hide each
-// other's LDS and barrier latency (measured faster than 256x256 with one wave
-// of 128x128 per SIMD, which holds 256 accumulators per lane in AGPRs).
+// Large problems use 256x256 blocks of 8 waves (64x128 wave tiles): two waves
+// per SIMD hide each other's LDS and barrier latency (measured faster than one
+// 128x128 wave per SIMD, which holds 256 accumulators per lane in AGPRs).
 //
 // Operands are copied into LDS exactly as they are stored (b128 copies, no
-// transposition): K-contiguous operands as [row][BK+8], M/N-contiguous ones as
-// [k][cols+16].  An MFMA 16x16x32 operand is 8 halves per lane; lane 16g+r
-// takes row/col r and the k values {4g..4g+3} U {16+4g..16+4g+3} of the
-// 32-wide step (any k permutation is exact as long as A and B agree), read as
-// two 4-half pieces:
-//   * K-contiguous tile: ds_read_b64 of [row r][16h + 4g .. +3];
-//   * M/N-contiguous tile: ds_read_b64_tr_b16.  Within each 16-lane group,
-//     destination lane d = 4a+e receives element e of the 8-byte chunks read
-//     by source lanes a, a+4, a+8, a+12; so when source lane s reads
-//     [k = 16h + 4g + s/4][c0 + 4(s%4) .. +3], lane d receives the four k of
-//     column c0 + d.
-// With these k sets, the lanes of one half-wave read 8 consecutive k rows of
-// an M/N-contiguous tile whose row stride is 8 banks apart: conflict-free.
+// transposition): K-contiguous operands as swizzled [row][64], M/N-contiguous
+// ones as [k][cols+16].  An MFMA 16x16x32 operand is 8 halves per lane; lane
+// 16g+r takes row/col r and k = 8g .. 8g+7 of the 32-wide step:
+//   * K-contiguous tile: one ds_read_b128 of [row r][8g .. 8g+7] (swizzled);
+//   * M/N-contiguous tile: two ds_read_b64_tr_b16.  Within each 16-lane
+//     group, destination lane d = 4a+e receives element e of the 8-byte chunks
+//     read by source lanes a, a+4, a+8, a+12; so when source lane s reads
+//     [k = 8g + s/4 (+4)][c0 + 4(s%4) .. +3], lane d receives four
+//     consecutive k of column c0 + d.
+// All of these access patterns were measured conflict-free on gfx950 (a b128
+// read moves twice the bytes per LDS cycle of a b64 read, so K-contiguous
+// fragments use one b128).
 //
 // For TN with a colsum target, the blocks of the first M tile also sum their
 // LDS B tiles over k (db = 1ᵀ·δ in f32, no extra HBM pass).  Split-K slices
@@ -45,9 +44,8 @@ typedef short s4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int BK = 32;
-constexpr int KPAD = 8;   // K-contiguous rows: 40 halves = 20 dwords
-constexpr int MPAD = 16;  // M/N-contiguous rows: cols + 16 halves
+constexpr int BK = 64;    // K per LDS stage: two 32-wide MFMA k-steps
+constexpr int MPAD = 16;  // M/N-contiguous rows: cols + 16 halves (8 banks)
 
 struct HalfArgs {
   const unsigned short* A;
@@ -111,15 +109,22 @@ __device__ inline u2 lds_tr(const unsigned short* p) {
 
 // One operand of the block: tile geometry and its global <-> LDS movement.
 // ROWS = BM (A) or BN (B); KC = stored K-contiguous.
+//
+// K-contiguous tiles are [row][64 halves] with no padding; the eight 16-byte
+// granules of a row are stored at granule ^ ((row >> 1) & 7), which makes the
+// fragment reads (16 consecutive rows, one granule each) and the tile writes
+// conflict-free.  M/N-contiguous tiles are [k][ROWS + 16].
 template <int ROWS, bool KC, int THREADS>
 struct Operand {
-  static constexpr int STRIDE = KC ? (BK + KPAD) : (ROWS + MPAD);  // halves per LDS row
+  static constexpr int STRIDE = KC ? BK : (ROWS + MPAD);  // halves per LDS row
   static constexpr int ELEMS = KC ? ROWS * STRIDE : BK * STRIDE;
   static constexpr int CHUNKS = ROWS * BK / 8;  // b128 per tile
   static constexpr int PER_THREAD = CHUNKS / THREADS;
   static_assert(CHUNKS % THREADS == 0, "tile must split evenly over threads");
 
   u4 v[PER_THREAD];
+
+  __device__ static inline int swz(int row, int granule) { return (granule ^ ((row >> 1) & 7)) * 8; }
 
   // Global (rows r0.., k0..) -> registers.
   __device__ inline void load(const unsigned short* base, int ld, int r0, int k0, int rows, int ke, bool full,
@@ -141,25 +146,24 @@ struct Operand {
     for (int i = 0; i < PER_THREAD; ++i) {
       const int idx = tid + THREADS * i;
       if constexpr (KC) {
-        *reinterpret_cast<u4*>(&lds[(idx / (BK / 8)) * STRIDE + 8 * (idx % (BK / 8))]) = v[i];
+        const int row = idx / (BK / 8), kc = idx % (BK / 8);
+        *reinterpret_cast<u4*>(&lds[row * STRIDE + swz(row, kc)]) = v[i];
       } else {
         *reinterpret_cast<u4*>(&lds[(idx / (ROWS / 8)) * STRIDE + 8 * (idx % (ROWS / 8))]) = v[i];
       }
     }
   }
-  // MFMA operand (8 halves) of the 16 rows [rbase, rbase+16) for lane (g, r).
-  __device__ inline u4 frag(const unsigned short* lds, int rbase, int g, int r) const {
-    u2 lo, hi;
+  // MFMA operand (8 halves) of k-step kk (k in [32kk, 32kk+32)) for the 16
+  // rows [rbase, rbase+16), lane (g, r): k = 32kk + 8g .. 32kk + 8g + 7.
+  __device__ inline u4 frag(const unsigned short* lds, int kk, int rbase, int g, int r) const {
     if constexpr (KC) {
-      const unsigned short* p = &lds[(rbase + r) * STRIDE + 4 * g];
-      lo = *reinterpret_cast<const u2*>(p);
-      hi = *reinterpret_cast<const u2*>(p + 16);
+      const int row = rbase + r;
+      return *reinterpret_cast<const u4*>(&lds[row * STRIDE + swz(row, 4 * kk + g)]);
     } else {
-      const unsigned short* p = &lds[(4 * g + (r >> 2)) * STRIDE + rbase + 4 * (r & 3)];
-      lo = lds_tr(p);
-      hi = lds_tr(p + 16 * STRIDE);
+      const unsigned short* p = &lds[(32 * kk + 8 * g + (r >> 2)) * STRIDE + rbase + 4 * (r & 3)];
+      const u2 lo = lds_tr(p), hi = lds_tr(p + 4 * STRIDE);
+      return u4{lo[0], lo[1], hi[0], hi[1]};
     }
-    return u4{lo[0], lo[1], hi[0], hi[1]};
   }
 };
 
@@ -215,12 +219,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_kernel(HalfArgs p) {
     for (int u = 0; u < TN; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < BK / 32; ++kk) {
     u4 bf[TN];
 #pragma unroll
-    for (int u = 0; u < TN; ++u) bf[u] = ob.frag(sB(buf), wn + 16 * u, g, r);
+    for (int u = 0; u < TN; ++u) bf[u] = ob.frag(sB(buf), kk, wn + 16 * u, g, r);
 #pragma unroll
     for (int t = 0; t < TM; ++t) {
-      const u4 af = oa.frag(sA(buf), wm + 16 * t, g, r);
+      const u4 af = oa.frag(sA(buf), kk, wm + 16 * t, g, r);
 #pragma unroll
       for (int u = 0; u < TN; ++u) {
         if constexpr (IS_BF16)
@@ -230,6 +236,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_kernel(HalfArgs p) {
           acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, af),
                                                              __builtin_bit_cast(f16x8, bf[u]), acc[t][u], 0, 0, 0);
       }
+    }
     }
   };
 
@@ -361,13 +368,13 @@ hipError_t launch_cfg(hipStream_t s, HalfArgs a, int splits, bool bf16) {
 
 template <bool A_KC, bool B_KC>
 hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16) {
-  // 128x256 blocks of 8 waves (2 per SIMD, 64x64 wave tiles) once they give
-  // at least one block per CU -- the fastest of the measured shapes for all
-  // three layouts at 8192x4096x4096; 128x128 (4 waves) for mid sizes; 64x64
-  // for small ones.
-  const long long tbig = (long long)((a.M + 127) / 128) * ((a.N + 255) / 256) * splits;
+  // 256x256 blocks of 8 waves (2 per SIMD, 64x128 wave tiles) when they give
+  // at least one block per CU -- the fastest measured shape for all three
+  // layouts at 8192x4096x4096; 128x128 (4 waves) for mid sizes; 64x64 for
+  // small ones.
+  const long long tbig = (long long)((a.M + 255) / 256) * ((a.N + 255) / 256) * splits;
   const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
-  if (tbig >= 256) return launch_cfg<128, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16);
+  if (tbig >= 256) return launch_cfg<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
   if (t128 >= 128) return launch_cfg<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
   return launch_cfg<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
 }
