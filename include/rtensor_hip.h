@@ -171,7 +171,8 @@ int rt_mlp_logits(rt_mlp* mlp, float* host, size_t n);
  * losses summed in row order.  Returns RT_ERR_LABEL if a label was >= C. */
 int rt_mlp_last_loss(rt_mlp* mlp, float* out);
 /* GpuMlp::weights / grads (mod.rs:1534-1551): blocking; host[i] receives
- * parameter i of [W1, b1, W2, b2, ...] (f32; the master copy for bf16). */
+ * parameter i of [W1, b1, W2, b2, ...] (f32; the master copy for bf16;
+ * gradients are reported unscaled when a loss scale is set). */
 int rt_mlp_weights(rt_mlp* mlp, float* const* host, int n);
 int rt_mlp_grads(rt_mlp* mlp, float* const* host, int n);
 /* GpuMlp::dispatches_por_passo (mod.rs:1559-1561): kernel launches per step. */

@@ -69,6 +69,9 @@ struct rt_mlp {
   float* partials = nullptr;
   size_t partial_elems = 0;
   float* loss_rows = nullptr;
+  // Mixed precision: [0] applied Adam updates, [1] overflow flag of the last
+  // step, [2] a step was issued (see step_begin_launch).
+  int* state = nullptr;
   int t = 0;
   int dispatches = 0;
   bool mixed = false;
@@ -229,6 +232,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   }
   size_t o_part = reserve(part * 4);
   size_t o_loss = reserve(batch * 4);
+  size_t o_state = reserve(16 * 4);
 
   hipError_t e = hipSetDevice(c->device);
   if (e == hipSuccess) e = hipMalloc(&p->arena, bytes);
@@ -248,6 +252,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   }
   p->partials = part ? (float*)(p->arena + o_part) : nullptr;
   p->loss_rows = (float*)(p->arena + o_loss);
+  p->state = (int*)(p->arena + o_state);
 
   // Zero everything (padding and moments must start at 0), then upload θ.
   e = fill_i32_launch(c->stream, (int*)p->arena, 0, bytes / 4);
@@ -275,7 +280,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   }
   n += 1;  // softmax-xent
   n += 1;  // optimizer
-  if (p->mixed) n += 2;  // overflow flag reset + non-finite check
+  if (p->mixed) n += 2;  // step prologue + non-finite check
   p->dispatches = n;
   c->mlps.push_back(p);
   *out = p;
@@ -310,12 +315,12 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   const int nl = p->n_layers;
   const int B = (int)p->batch;
   const float scale = p->mixed ? p->cfg.loss_scale : 1.0f;
-  int* overflow = c->d_flags + 1;
+  int* overflow = p->state + 1;
 
   if (p->mixed) {
-    Launch Lz(c, "overflow_reset");
-    hipError_t e = fill_i32_launch(c->stream, overflow, 0, 1);
-    if (e != hipSuccess) return hip_fail(c, e, "overflow reset");
+    Launch Lz(c, "step_begin");
+    hipError_t e = step_begin_launch(c->stream, p->state);
+    if (e != hipSuccess) return hip_fail(c, e, "step prologue");
   }
   if ((rc = run_forward(p, x))) return rc;
 
@@ -372,8 +377,12 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     P.inv_c2 = 1.0f / c2;
   }
   if (p->mixed) {
+    // Unscale exactly (the loss scale is a power of two in practice) and skip
+    // the whole update on a non-finite gradient; a skipped step does not
+    // advance Adam's t (the count lives on the device).
     P.grad_scale = 1.0f / p->cfg.loss_scale;
     P.skip_flag = overflow;
+    P.device_t = p->state;
   }
   if (P.kind == 1 && P.momentum == 0.0f) T.m = nullptr;
   Launch Lz(c, "optimizer");
@@ -446,7 +455,16 @@ int rt_mlp_weights(rt_mlp* p, float* const* host, int n) {
 
 int rt_mlp_grads(rt_mlp* p, float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
-  return fetch(p, p->grad, host, n);
+  int rc = fetch(p, p->grad, host, n);
+  if (rc || !p->mixed || p->cfg.loss_scale == 1.0f) return rc;
+  // Gradients are held scaled by the loss scale; report dL/dθ.
+  const float inv = 1.0f / p->cfg.loss_scale;
+  for (int l = 0; l < p->n_layers; ++l) {
+    const Layer& Ly = p->L[l];
+    for (size_t i = 0; i < Ly.din * Ly.dout; ++i) host[2 * l][i] *= inv;
+    for (size_t i = 0; i < Ly.dout; ++i) host[2 * l + 1][i] *= inv;
+  }
+  return RT_OK;
 }
 
 int rt_mlp_dispatches(rt_mlp* p, int* out) {
@@ -459,7 +477,7 @@ int rt_mlp_overflow(rt_mlp* p, int* out) {
   if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
   rt_ctx* c = p->ctx;
   int flag = 0;
-  hipError_t e = hipMemcpyAsync(&flag, c->d_flags + 1, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+  hipError_t e = hipMemcpyAsync(&flag, p->state + 1, sizeof(int), hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "overflow flag");
   *out = flag;

@@ -38,8 +38,25 @@ __device__ inline unsigned short f32_to_bf16_rne(float x) {
   return (unsigned short)(u >> 16);
 }
 
+__device__ inline float powi_dev(float a, int b) {
+  float r = 1.0f;
+  for (;;) {
+    if (b & 1) r *= a;
+    b /= 2;
+    if (b == 0) break;
+    a *= a;
+  }
+  return r;
+}
+
 __global__ __launch_bounds__(kThreads) void optimizer_kernel(OptBatch b) {
   if (b.p.skip_flag != nullptr && *b.p.skip_flag != 0) return;
+  float inv_c1 = b.p.inv_c1, inv_c2 = b.p.inv_c2;
+  if (b.p.device_t != nullptr) {
+    const int t = *b.p.device_t + 1;
+    inv_c1 = 1.0f / (1.0f - powi_dev(b.p.beta1, t));
+    inv_c2 = 1.0f / (1.0f - powi_dev(b.p.beta2, t));
+  }
   const int blk = blockIdx.x;
   int ti = 0;
   while (ti + 1 < b.nt && b.block_start[ti + 1] <= blk) ++ti;
@@ -57,8 +74,8 @@ __global__ __launch_bounds__(kThreads) void optimizer_kernel(OptBatch b) {
       const float vi = T.v[i] * P.beta2 + (g * g) * (1.0f - P.beta2);
       T.m[i] = mi;
       T.v[i] = vi;
-      const float m_hat = mi * P.inv_c1;
-      const float v_hat = vi * P.inv_c2;
+      const float m_hat = mi * inv_c1;
+      const float v_hat = vi * inv_c2;
       th = th - (m_hat / (sqrtf(v_hat) + P.eps)) * P.lr;
     } else if (P.momentum == 0.0f) {
       th = th - g * P.lr;
@@ -91,9 +108,22 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(NonFiniteArgs a) {
   if (bad) *a.flag = 1;
 }
 
+__global__ void step_begin_kernel(int* state) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    if (state[2] != 0 && state[1] == 0) state[0] += 1;
+    state[2] = 1;
+    state[1] = 0;
+  }
+}
+
 }  // namespace
 
 namespace rt {
+
+hipError_t step_begin_launch(hipStream_t s, int* state) {
+  hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(64), 0, s, state);
+  return hipGetLastError();
+}
 
 float powi_f32(float a, int b) {
   // Square-and-multiply from the least significant exponent bit, as f32::powi

@@ -84,3 +84,34 @@ def numpy_f32_trajectory(params, batches, lr, beta1=0.9, beta2=0.999, eps=1e-8):
             v[i] = v[i] * f(beta2) + (g * g) * (f(1) - f(beta2))
             ps[i] -= ((m[i] * (f(1) / c1)) / (np.sqrt(v[i] * (f(1) / c2)) + f(eps))) * f(lr)
     return ps, losses
+
+
+def bf16_pipeline_grads(params, x, lab, loss_scale=1024.0):
+    """Step-1 gradients of the ReLU MLP computed in float64 with the rounding
+    points of the mixed-precision plan: bf16 weights and inputs, hidden
+    activations stored as bf16 (round to nearest even), δ stored as bf16 after
+    the loss and after every ReLU mask; gradients unscaled at the end.  An
+    independent restatement of what the bf16 training step computes."""
+    from rgpu_amd.gpu import bf16_bits_to_f32, f32_to_bf16_bits
+
+    def rb(a):
+        return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(a, np.float32))).astype(np.float64)
+
+    Ws = [rb(p) for p in params[0::2]]
+    bs = [np.asarray(p, np.float64).reshape(1, -1) for p in params[1::2]]
+    acts = [rb(x)]
+    for l in range(len(Ws)):
+        z = acts[-1] @ Ws[l] + bs[l]
+        acts.append(rb(np.maximum(z, 0)) if l < len(Ws) - 1 else z)
+    z = acts[-1]
+    p = np.exp(z - z.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    B = z.shape[0]
+    d = rb((p - np.eye(z.shape[1])[lab]) * (loss_scale / B))
+    grads = [None] * (2 * len(Ws))
+    for l in reversed(range(len(Ws))):
+        grads[2 * l] = acts[l].T @ d / loss_scale
+        grads[2 * l + 1] = d.sum(0, keepdims=True) / loss_scale
+        if l > 0:
+            d = rb((d @ Ws[l].T) * (acts[l] > 0))
+    return grads
