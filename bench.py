@@ -1,6 +1,6 @@
 """Benchmark of the MLP training step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-bwd]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only all|step|bwd|splitk|mixed]
 
 Workload (one "step"): MLP 512->1024(ReLU)->1024(ReLU)->10, f32, batch 2048,
 softmax cross-entropy, Adam(1e-3, 0.9, 0.999, 1e-8): forward, backward and the
@@ -13,6 +13,10 @@ better).  Next to it:
                 over its average HIP-event duration, against the f32 MFMA peak
   bwd_gemm      Linear 4096->4096 backward at batch 8192 in bf16 (dX = dY·Wᵀ,
                 dW = Xᵀ·dY with db fused), TFLOP/s against the bf16 MFMA peak
+  splitk_dw     dW = Xᵀ·dY, K = 262144, f16 in / f32 out, db fused, against
+                the HBM roofline
+  mixed_mlp     8 x 4096 ReLU MLP -> 1000 classes, batch 4096, bf16 with f32
+                master weights, loss scale 1024, Adam: ms/step and TFLOP/s
   cpu_baseline  the CPU oracle (C++ restatement of rtensor's single-threaded
                 CPU path) timed on a bounded sample of the same workload
 """
@@ -144,6 +148,65 @@ def bench_bwd_gemm(gpu, G, reps=20):
     }
 
 
+def bench_splitk(gpu, G, reps=10, slices=64):
+    """Split-K weight gradient over a 262144-long batch, f16 operands."""
+    K, M, N = 262144, 512, 512
+    rng = np.random.default_rng(4)
+    x = gpu.upload(rng.standard_normal((K, M), dtype=np.float32) / np.float32(16.0), G.F16)
+    dy = gpu.upload(rng.standard_normal((K, N), dtype=np.float32) / np.float32(16.0), G.F16)
+    dw, db = gpu.zeros((M, N)), gpu.zeros((1, N))
+    part = gpu.zeros((slices * (M * N + N),))
+    for _ in range(2):
+        gpu.split_k(x, dy, dw, part, slices, True, colsum=db)
+    gpu.sync()
+    gpu.profile_reset()
+    gpu.profile(True)
+    for _ in range(reps):
+        gpu.split_k(x, dy, dw, part, slices, True, colsum=db)
+    gpu.sync()
+    gpu.profile(False)
+    prof = {n: ms / c for n, c, ms in gpu.perfilar()}
+    gpu.profile_reset()
+    t = prof["splitk_gemm"] + prof.get("splitk_reduce", 0.0)
+    bytes_ = 2 * K * M * 2 + M * N * 4 + N * 4  # compulsory: read X, dY; write dW, db
+    gbs = bytes_ / (t * 1e-3) / 1e9
+    flops = 2.0 * K * M * N
+    return {"config": "dW = X^T dY, K=262144, X,dY f16 [262144,512] ~N(0,1)/16, f32 out [512,512], db fused",
+            "slices": slices, "gemm_ms": round(prof["splitk_gemm"], 4),
+            "reduce_ms": round(prof.get("splitk_reduce", 0.0), 4), "ms": round(t, 4),
+            "bound": "hbm", "achieved_gbs": round(gbs, 1), "peak_gbs": PEAK_HBM_GBS,
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
+
+
+def bench_mixed(gpu, G, steps=20, warmup=3):
+    """8 x 4096 ReLU layers -> 1000 classes, batch 4096, bf16 + f32 master, Adam."""
+    dims = [4096] * 9 + [1000]
+    B = 4096
+    rng = np.random.default_rng(5)
+    params = []
+    for l in range(len(dims) - 1):
+        params += [kaiming(rng, dims[l], dims[l + 1]), np.zeros((1, dims[l + 1]), np.float32)]
+    mlp = G.GpuMlp.from_params(gpu, params, B, 1e-3, precision="bf16", loss_scale=1024.0)
+    del params
+    xs = [gpu.upload(rng.standard_normal((B, dims[0]), dtype=np.float32), G.BF16) for _ in range(4)]
+    ys = [G.upload_labels(gpu, rng.integers(0, dims[-1], B)) for _ in range(4)]
+    for i in range(warmup):
+        mlp.step(xs[i % 4], ys[i % 4])
+    gpu.sync()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        mlp.step(xs[i % 4], ys[i % 4])
+    gpu.sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    flops = step_flops(dims, B)
+    loss = mlp.last_loss()
+    mlp.destroy()
+    return {"config": "MLP 8x4096(ReLU) -> 1000, batch 4096, bf16 weights/activations, f32 master, "
+                      "loss scale 1024, Adam(1e-3)", "ms_per_step": round(ms, 3),
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "peak_tflops": PEAK_BF16_TFLOPS,
+            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "final_loss": round(float(loss), 4)}
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's single-threaded training step on the host, bounded sample."""
     from oracle import oracle as O
@@ -185,7 +248,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-bwd", action="store_true")
+    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed"], default="all",
+                    help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the data-parallel "
@@ -195,6 +259,10 @@ def main():
     from rgpu_amd import gpu as G
 
     gpu = G.Gpu(0)
+    if args.only in ("bwd", "splitk", "mixed"):
+        fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed}[args.only]
+        print(json.dumps({args.only: fn(gpu, G)}), flush=True)
+        return
     wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
     ms = wall / args.steps * 1e3
     total_flops = step_flops(DIMS, BATCH)
@@ -241,8 +309,10 @@ def main():
         "roofline": roof,
         "kernels_us": kernels,
     }
-    if not args.no_bwd:
+    if args.only == "all":
         out["bwd_gemm"] = bench_bwd_gemm(gpu, G)
+        out["splitk_dw"] = bench_splitk(gpu, G)
+        out["mixed_mlp"] = bench_mixed(gpu, G)
     if not args.no_cpu:
         cb = cpu_baseline()
         out["cpu_baseline"] = cb
