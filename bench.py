@@ -207,6 +207,18 @@ def bench_mixed(gpu, G, steps=20, warmup=3):
             "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "final_loss": round(float(loss), 4)}
 
 
+def bench_copy(gpu, G, mib=256, reps=5):
+    """A plain device copy of known size (f32 -> f32 through the convert
+    kernel): reads and writes exactly mib MiB per launch.  Used to calibrate
+    the FETCH_SIZE / WRITE_SIZE counters."""
+    n = mib * 1024 * 1024 // 4
+    src, dst = gpu.zeros((n,)), gpu.zeros((n,))
+    for _ in range(reps):
+        gpu.convert(src, dst)
+    gpu.sync()
+    return {"bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4, "launches": reps}
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's single-threaded training step on the host, bounded sample."""
     from oracle import oracle as O
@@ -248,7 +260,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed"], default="all",
+    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy"], default="all",
                     help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -259,8 +271,8 @@ def main():
     from rgpu_amd import gpu as G
 
     gpu = G.Gpu(0)
-    if args.only in ("bwd", "splitk", "mixed"):
-        fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed}[args.only]
+    if args.only in ("bwd", "splitk", "mixed", "copy"):
+        fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed, "copy": bench_copy}[args.only]
         print(json.dumps({args.only: fn(gpu, G)}), flush=True)
         return
     wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
