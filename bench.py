@@ -58,7 +58,11 @@ def step_flops(dims, batch):
 
 
 def label_flops(label, dims, batch):
-    """FLOPs per launch of a plan kernel label (fwd_l*, dw_l*, dx_l*)."""
+    """FLOPs per launch of a plan kernel label (fwd_l*, dw_l*, dx_l*, and
+    dwdx_l*: a layer's dW and dX in one launch)."""
+    if label.startswith("dwdx_l"):
+        l = int(label[len("dwdx_l"):])
+        return 2 * 2 * batch * dims[l] * dims[l + 1]
     for pre in ("fwd_l", "dw_l", "dx_l"):
         if label.startswith(pre):
             l = int(label[len(pre):])

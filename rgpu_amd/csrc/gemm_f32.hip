@@ -30,7 +30,7 @@
 // RELU_BWD, kernels.rs:119-131).  For TN with a colsum target the blocks of
 // the first M tile also sum the B tiles they stage in LDS over K: that is
 // db = 1ᵀ·δ (COLSUM, kernels.rs:182-199) at no extra HBM traffic.
-// With blockIdx.z > 0 splits, each slice writes a raw f32 partial plane and
+// With more than one K slice, each slice writes a raw f32 partial plane and
 // splitk_reduce sums the planes in slice order (REDUZ, splitk.rs:240-256):
 // deterministic, no float atomics.
 
@@ -51,12 +51,18 @@ struct F32Args {
   int epi;
   const float* bias;
   const float* mask;
-  float* colsum;  // [N], or [splits, N] partial rows when gridDim.z > 1
+  float* colsum;  // [N], or [splits, N] partial rows when splits > 1
   int k_per_split;
   long long split_stride;
-  int tiles_m, tiles_n;
+  int tiles_m, tiles_n, splits;
   int vec_a, vec_b, vec_c;
 };
+
+// Consecutive workgroups go to different XCDs (round robin over 8), each
+// with its own L2.  Renumber so that every XCD gets a contiguous run of
+// tile indices; the grouped raster below then keeps the tiles resident on
+// one XCD sharing A rows and B columns.
+__device__ inline int xcd_local(int bid, int nb) { return (nb & 7) == 0 ? (bid & 7) * (nb >> 3) + (bid >> 3) : bid; }
 
 // Loads `cnt` consecutive floats (cnt = 1, 2 or 4) from LDS as one access.
 template <int CNT>
@@ -84,32 +90,35 @@ __device__ inline f4 load4(const float* base, int ld, int row, int col, int rows
   return v;
 }
 
+// One block's work: tile `bid` (already XCD-renumbered, in [0, tiles)) of
+// K slice `split`.  smem holds the two LDS stages of both operands.
 template <int BM, int BN, bool A_KC, bool B_KC>
-__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
-  constexpr int BK = 32, PAD = 4;
-  constexpr int TM = BM / 32, TN = BN / 32;  // MFMA tiles per wave (2x2 waves of BM/2 x BN/2)
-  constexpr int A_STRIDE = A_KC ? (BK + PAD) : (BM + PAD);
-  constexpr int B_STRIDE = B_KC ? (BK + PAD) : (BN + PAD);
-  constexpr int A_ELEMS = A_KC ? BM * A_STRIDE : BK * A_STRIDE;
-  constexpr int B_ELEMS = B_KC ? BN * B_STRIDE : BK * B_STRIDE;
-  constexpr int A_LD = BM / 32, B_LD = BN / 32;  // float4 loads per thread per K step
+struct F32Tile {
+  static constexpr int BK = 32, PAD = 4;
+  static constexpr int TM = BM / 32, TN = BN / 32;  // MFMA tiles per wave (2x2 waves of BM/2 x BN/2)
+  static constexpr int A_STRIDE = A_KC ? (BK + PAD) : (BM + PAD);
+  static constexpr int B_STRIDE = B_KC ? (BK + PAD) : (BN + PAD);
+  static constexpr int A_ELEMS = A_KC ? BM * A_STRIDE : BK * A_STRIDE;
+  static constexpr int B_ELEMS = B_KC ? BN * B_STRIDE : BK * B_STRIDE;
+  static constexpr int SMEM = 2 * (A_ELEMS + B_ELEMS);  // floats
+  static constexpr int A_LD = BM / 32, B_LD = BN / 32;  // float4 loads per thread per K step
   static_assert(BM % 32 == 0 && BN % 32 == 0 && BM <= 128 && BN <= 128, "tile");
 
-  __shared__ __attribute__((aligned(16))) float sA[2][A_ELEMS];
-  __shared__ __attribute__((aligned(16))) float sB[2][B_ELEMS];
+  __device__ static void run(const F32Args& p, int bid, int split, float* smem);
+};
+
+template <int BM, int BN, bool A_KC, bool B_KC>
+__device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int split, float* smem) {
+  float* const sA0 = smem;
+  float* const sB0 = smem + 2 * A_ELEMS;
+  auto sA = [&](int buf) { return sA0 + buf * A_ELEMS; };
+  auto sB = [&](int buf) { return sB0 + buf * B_ELEMS; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, r = lane & 15;
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
 
-  // Tile order.  Consecutive workgroups go to different XCDs (round robin
-  // over 8), each with its own L2: renumber so every XCD gets a contiguous
-  // run of tiles, then raster that run in groups of 8 M-tiles so the tiles
-  // resident on one XCD share A rows and B columns.
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   constexpr int GROUP = 8;
   const int per_group = GROUP * p.tiles_n;
   const int grp = bid / per_group;
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
   const int tile_n = in_grp / gsize;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
 
-  const int kb = blockIdx.z * p.k_per_split;
+  const int kb = split * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
 
@@ -157,20 +166,20 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
     for (int i = 0; i < A_LD; ++i) {
       const int idx = tid + kThreads * i;
       if constexpr (A_KC) {
-        *reinterpret_cast<f4*>(&sA[buf][(idx >> 3) * A_STRIDE + 4 * (idx & 7)]) = ra[i];
+        *reinterpret_cast<f4*>(&sA(buf)[(idx >> 3) * A_STRIDE + 4 * (idx & 7)]) = ra[i];
       } else {
         constexpr int Q = BM / 4;
-        *reinterpret_cast<f4*>(&sA[buf][(idx / Q) * A_STRIDE + 4 * (idx % Q)]) = ra[i];
+        *reinterpret_cast<f4*>(&sA(buf)[(idx / Q) * A_STRIDE + 4 * (idx % Q)]) = ra[i];
       }
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
       const int idx = tid + kThreads * i;
       if constexpr (B_KC) {
-        *reinterpret_cast<f4*>(&sB[buf][(idx >> 3) * B_STRIDE + 4 * (idx & 7)]) = rb[i];
+        *reinterpret_cast<f4*>(&sB(buf)[(idx >> 3) * B_STRIDE + 4 * (idx & 7)]) = rb[i];
       } else {
         constexpr int Q = BN / 4;
-        *reinterpret_cast<f4*>(&sB[buf][(idx / Q) * B_STRIDE + 4 * (idx % Q)]) = rb[i];
+        *reinterpret_cast<f4*>(&sB(buf)[(idx / Q) * B_STRIDE + 4 * (idx % Q)]) = rb[i];
       }
     }
   };
@@ -182,8 +191,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
     for (int u = 0; u < TN; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](int buf) {
-    const float* as = sA[buf];
-    const float* bs = sB[buf];
+    const float* as = sA(buf);
+    const float* bs = sB(buf);
 #pragma unroll
     for (int ss = 0; ss < BK / 16; ++ss) {
       float af[TM][4], bf[TN][4];
@@ -236,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
       compute(cur);
       if constexpr (!B_KC) {
         if (do_cs) {
-          const float* bs = sB[cur];
+          const float* bs = sB(cur);
 #pragma unroll 8
           for (int kk = 0; kk < BK; ++kk) cs += bs[kk * B_STRIDE + tid];
         }
@@ -246,11 +255,11 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
     }
   }
 
-  if (do_cs && n0 + tid < p.N) p.colsum[(long long)blockIdx.z * p.N + n0 + tid] = cs;
+  if (do_cs && n0 + tid < p.N) p.colsum[(long long)split * p.N + n0 + tid] = cs;
 
   // Epilogue.  Lane owns rows m0+wm+TM*(4g+q)+t and columns n0+wn+TN*r+u.
-  const bool partial = gridDim.z > 1;
-  float* Cout = p.C + (long long)blockIdx.z * p.split_stride;
+  const bool partial = p.splits > 1;
+  float* Cout = p.C + (long long)split * p.split_stride;
   const int col0 = n0 + wn + TN * r;
   float bias_v[TN];
 #pragma unroll
@@ -294,6 +303,36 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
   }
 }
 
+template <int BM, int BN, bool A_KC, bool B_KC>
+__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
+  using T = F32Tile<BM, BN, A_KC, B_KC>;
+  __shared__ __attribute__((aligned(16))) float smem[T::SMEM];
+  T::run(p, xcd_local(blockIdx.x, gridDim.x), blockIdx.z, smem);
+}
+
+// Two independent GEMMs in one launch (horizontal fusion): blocks
+// [0, n0) run problem 0, the rest problem 1, each problem's split index
+// folded into its block range.  n0 is a multiple of 8 so both problems are
+// spread evenly over the XCDs; problem 0 is dispatched first.
+template <class T0, class T1>
+__global__ __launch_bounds__(kThreads) void gemm_f32_pair_kernel(F32Args p0, F32Args p1, int n0) {
+  constexpr int S = T0::SMEM > T1::SMEM ? T0::SMEM : T1::SMEM;
+  __shared__ __attribute__((aligned(16))) float smem[S];
+  const int b = blockIdx.x;
+  if (b < n0) {
+    const int tiles = p0.tiles_m * p0.tiles_n;
+    const int nb = tiles * p0.splits;
+    if (b >= nb) return;  // padding up to a multiple of 8
+    const int loc = xcd_local(b, nb);
+    T0::run(p0, loc % tiles, loc / tiles, smem);
+  } else {
+    const int tiles = p1.tiles_m * p1.tiles_n;
+    const int nb = tiles * p1.splits;
+    const int loc = xcd_local(b - n0, nb);
+    T1::run(p1, loc % tiles, loc / tiles, smem);
+  }
+}
+
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, long long stride,
                                                              int M, int N, float* C, int ldc, int epi,
                                                              const float* bias, const float* mask,
@@ -322,29 +361,35 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 }
 
 template <int BM, int BN, bool A_KC, bool B_KC>
-hipError_t launch_f32(hipStream_t s, F32Args a, int splits) {
+hipError_t launch_f32(hipStream_t s, F32Args a) {
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
-  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+  dim3 grid(a.tiles_m * a.tiles_n, 1, a.splits);
   hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_KC, B_KC>), grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
-template <bool A_KC, bool B_KC>
-hipError_t dispatch_tile(hipStream_t s, F32Args a, int splits) {
-  // 128x128 tiles when they alone give at least two waves of 256 CUs,
-  // otherwise 64x64 (4x the workgroups) so small GEMMs still fill the chip.
-  const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
-  if (t128 >= 512) return launch_f32<128, 128, A_KC, B_KC>(s, a, splits);
-  if (a.N <= 32) return launch_f32<64, 32, A_KC, B_KC>(s, a, splits);
-  return launch_f32<64, 64, A_KC, B_KC>(s, a, splits);
+// 128x128 tiles when they alone give at least two waves of 256 CUs,
+// otherwise 64x64 (4x the workgroups) so small GEMMs still fill the chip;
+// 64x32 for narrow outputs.
+enum TileCfg { kT128, kT64x32, kT64 };
+TileCfg pick_tile(const F32Args& a) {
+  const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * a.splits;
+  if (t128 >= 512) return kT128;
+  if (a.N <= 32) return kT64x32;
+  return kT64;
 }
 
-}  // namespace
+template <bool A_KC, bool B_KC>
+hipError_t dispatch_tile(hipStream_t s, F32Args a) {
+  switch (pick_tile(a)) {
+    case kT128: return launch_f32<128, 128, A_KC, B_KC>(s, a);
+    case kT64x32: return launch_f32<64, 32, A_KC, B_KC>(s, a);
+    default: return launch_f32<64, 64, A_KC, B_KC>(s, a);
+  }
+}
 
-namespace rt {
-
-hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d) {
+F32Args make_args(const rt::GemmDesc& d) {
   F32Args a{};
   a.A = static_cast<const float*>(d.A);
   a.B = static_cast<const float*>(d.B);
@@ -359,22 +404,66 @@ hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d) {
   a.bias = d.bias;
   a.mask = static_cast<const float*>(d.mask);
   a.colsum = d.splits > 1 ? d.colsum_partials : d.colsum;
-  const int splits = d.splits < 1 ? 1 : d.splits;
+  a.splits = d.splits < 1 ? 1 : d.splits;
   // Slices are whole multiples of the 32-wide K step.
-  int kps = (d.K + splits - 1) / splits;
+  int kps = (d.K + a.splits - 1) / a.splits;
   kps = ((kps + 31) / 32) * 32;
-  a.k_per_split = splits > 1 ? kps : (d.K > 0 ? d.K : 1);
+  a.k_per_split = a.splits > 1 ? kps : (d.K > 0 ? d.K : 1);
   a.split_stride = d.split_stride;
   auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   a.vec_a = (d.lda % 4 == 0) && al16(d.A);
   a.vec_b = (d.ldb % 4 == 0) && al16(d.B);
   a.vec_c = (d.ldc % 4 == 0) && al16(d.C);
+  return a;
+}
+
+// The backward pair of a hidden layer: dW = Aᵀ·δ (TN, 64x64 or, for a
+// narrow layer, 64x32 tiles; any number of K slices) and
+// dX = (δ·Wᵀ) ⊙ mask (NT, 64x64 tiles, whole K).
+template <int BN0>
+hipError_t launch_pair_tn_nt(hipStream_t s, F32Args a0, F32Args a1) {
+  using T0 = F32Tile<64, BN0, false, false>;
+  using T1 = F32Tile<64, 64, true, true>;
+  a0.tiles_m = (a0.M + 63) / 64;
+  a0.tiles_n = (a0.N + BN0 - 1) / BN0;
+  a1.tiles_m = (a1.M + 63) / 64;
+  a1.tiles_n = (a1.N + 63) / 64;
+  const long long nb0 = (long long)a0.tiles_m * a0.tiles_n * a0.splits;
+  const long long nb1 = (long long)a1.tiles_m * a1.tiles_n * a1.splits;
+  const long long n0 = (nb0 + 7) / 8 * 8;
+  if (n0 + nb1 > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemm_f32_pair_kernel<T0, T1>), dim3((unsigned)(n0 + nb1)), dim3(kThreads), 0, s, a0, a1,
+                     (int)n0);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+namespace rt {
+
+hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d) {
+  const F32Args a = make_args(d);
   switch (d.layout) {
-    case RT_NN: return dispatch_tile<true, false>(s, a, splits);
-    case RT_TN: return dispatch_tile<false, false>(s, a, splits);
-    case RT_NT: return dispatch_tile<true, true>(s, a, splits);
+    case RT_NN: return dispatch_tile<true, false>(s, a);
+    case RT_TN: return dispatch_tile<false, false>(s, a);
+    case RT_NT: return dispatch_tile<true, true>(s, a);
   }
   return hipErrorInvalidValue;
+}
+
+bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1) {
+  if (d0.in_dtype != RT_F32 || d1.in_dtype != RT_F32) return false;
+  if (d0.layout != RT_TN || d1.layout != RT_NT || d1.splits > 1) return false;
+  // Only where the single launches would use the same tiles.
+  const TileCfg t0 = pick_tile(make_args(d0));
+  return (t0 == kT64 || t0 == kT64x32) && pick_tile(make_args(d1)) == kT64;
+}
+
+hipError_t gemm_pair_launch(hipStream_t s, const GemmDesc& d0, const GemmDesc& d1) {
+  if (!gemm_pair_supported(d0, d1)) return hipErrorInvalidValue;
+  const F32Args a0 = make_args(d0), a1 = make_args(d1);
+  if (pick_tile(a0) == kT64x32) return launch_pair_tn_nt<32>(s, a0, a1);
+  return launch_pair_tn_nt<64>(s, a0, a1);
 }
 
 hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M, int N,

@@ -80,9 +80,12 @@ __device__ inline float half_to_f32(unsigned short h) {
 }
 
 // 8 consecutive halves of a row-major matrix at (row, col); zero outside.
-__device__ inline u4 load8(const unsigned short* base, int ld, int row, int col, int rows, int cols, bool fast) {
+// One 16-byte load whenever the operand is 16-byte aligned (vec) and the whole
+// chunk is inside, so edge tiles stay vectorised except for their last chunk.
+__device__ inline u4 load8(const unsigned short* base, int ld, int row, int col, int rows, int cols, bool vec) {
   const unsigned short* src = base + (long long)row * ld + col;
-  if (fast) return *reinterpret_cast<const u4*>(src);
+  if (vec && row < rows && col + 8 <= cols) return *reinterpret_cast<const u4*>(src);
+  if (row >= rows) return u4{0u, 0u, 0u, 0u};
   unsigned short h[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) h[e] = (row < rows && col + e < cols) ? src[e] : (unsigned short)0;
@@ -127,17 +130,17 @@ struct Operand {
   __device__ static inline int swz(int row, int granule) { return (granule ^ ((row >> 1) & 7)) * 8; }
 
   // Global (rows r0.., k0..) -> registers.
-  __device__ inline void load(const unsigned short* base, int ld, int r0, int k0, int rows, int ke, bool full,
+  __device__ inline void load(const unsigned short* base, int ld, int r0, int k0, int rows, int ke, bool vec,
                               int tid) {
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
       const int idx = tid + THREADS * i;
       if constexpr (KC) {
         const int row = idx / (BK / 8), kc = idx % (BK / 8);
-        v[i] = load8(base, ld, r0 + row, k0 + 8 * kc, rows, ke, full);
+        v[i] = load8(base, ld, r0 + row, k0 + 8 * kc, rows, ke, vec);
       } else {
         const int kk = idx / (ROWS / 8), c = idx % (ROWS / 8);
-        v[i] = load8(base, ld, k0 + kk, r0 + 8 * c, ke, rows, full);
+        v[i] = load8(base, ld, k0 + kk, r0 + 8 * c, ke, rows, vec);
       }
     }
   }
@@ -202,14 +205,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_kernel(HalfArgs p) {
   const int kb = blockIdx.z * p.k_per_split;
   const int ke = min(p.K, kb + p.k_per_split);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
-  const bool rows_in = (m0 + BM <= p.M) && (n0 + BN <= p.N);
 
   OpA oa;
   OpB ob;
   auto load_tiles = [&](int k0) {
-    const bool full = rows_in && (k0 + BK <= ke);
-    oa.load(p.A, p.lda, m0, k0, p.M, ke, full && p.vec_a, tid);
-    ob.load(p.B, p.ldb, n0, k0, p.N, ke, full && p.vec_b, tid);
+    oa.load(p.A, p.lda, m0, k0, p.M, ke, p.vec_a, tid);
+    ob.load(p.B, p.ldb, n0, k0, p.N, ke, p.vec_b, tid);
   };
 
   f4 acc[TM][TN];

@@ -46,7 +46,8 @@ struct Layer {
   void* delta_h = nullptr;      // [batch, dout] bf16 (mixed precision)
   int splits_dw = 1;
   int splits_fwd = 1;
-  std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx;
+  bool pair_bwd = false;  // dW and dX of this layer in one launch
+  std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx, lbl_bwd;
 };
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -85,11 +86,11 @@ static bool valid_cfg(const rt_mlp_config* c) {
   return true;
 }
 
-// Run one GEMM of the plan, with optional split-K.
-static int plan_gemm(rt_mlp* p, const char* lbl, const char* lbl_red, int layout, int in_dtype, const void* A,
-                     const void* B, void* C, int out_dtype, int M, int N, int K, int lda, int ldb, int epi,
-                     const float* bias, const void* mask, int mask_dtype, float* colsum, int splits) {
-  rt_ctx* c = p->ctx;
+// One GEMM of the plan as a descriptor.  With splits > 1 it writes partial
+// planes into the plan's partials buffer, summed by finish_split.
+static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, const void* B, void* C, int out_dtype,
+                          int M, int N, int K, int lda, int ldb, int epi, const float* bias, const void* mask,
+                          int mask_dtype, float* colsum, int splits) {
   GemmDesc d;
   d.layout = layout;
   d.in_dtype = in_dtype;
@@ -109,26 +110,42 @@ static int plan_gemm(rt_mlp* p, const char* lbl, const char* lbl_red, int layout
     d.mask = mask;
     d.mask_dtype = mask_dtype;
     d.colsum = colsum;
-    Launch Lz(c, lbl);
-    hipError_t e = gemm_launch(c->stream, d);
-    if (e != hipSuccess) return hip_fail(c, e, lbl);
-    return RT_OK;
+    return d;
   }
   d.C = p->partials;
   d.out_dtype = RT_F32;
   d.splits = splits;
   d.split_stride = (long long)M * N;
   d.colsum_partials = colsum ? p->partials + (size_t)splits * M * N : nullptr;
+  // Where the reduction puts the result and what it applies.
+  d.epi = RT_EPI_NONE;
+  return d;
+}
+
+static int finish_split(rt_mlp* p, const GemmDesc& d, const char* lbl_red, void* C, int out_dtype, int epi,
+                        const float* bias, const void* mask, int mask_dtype, float* colsum) {
+  if (d.splits <= 1) return RT_OK;
+  rt_ctx* c = p->ctx;
+  Launch Lz(c, lbl_red);
+  hipError_t e = splitk_reduce_launch(c->stream, p->partials, d.splits, d.split_stride, d.M, d.N, C, out_dtype, d.N,
+                                      epi, bias, mask, mask_dtype, d.colsum_partials, colsum);
+  if (e != hipSuccess) return hip_fail(c, e, lbl_red);
+  return RT_OK;
+}
+
+// Run one GEMM of the plan, with optional split-K.
+static int plan_gemm(rt_mlp* p, const char* lbl, const char* lbl_red, int layout, int in_dtype, const void* A,
+                     const void* B, void* C, int out_dtype, int M, int N, int K, int lda, int ldb, int epi,
+                     const float* bias, const void* mask, int mask_dtype, float* colsum, int splits) {
+  rt_ctx* c = p->ctx;
+  const GemmDesc d = plan_desc(p, layout, in_dtype, A, B, C, out_dtype, M, N, K, lda, ldb, epi, bias, mask,
+                               mask_dtype, colsum, splits);
   {
     Launch Lz(c, lbl);
     hipError_t e = gemm_launch(c->stream, d);
     if (e != hipSuccess) return hip_fail(c, e, lbl);
   }
-  Launch Lz(c, lbl_red);
-  hipError_t e = splitk_reduce_launch(c->stream, p->partials, splits, (long long)M * N, M, N, C, out_dtype, N, epi,
-                                      bias, mask, mask_dtype, d.colsum_partials, colsum);
-  if (e != hipSuccess) return hip_fail(c, e, lbl_red);
-  return RT_OK;
+  return finish_split(p, d, lbl_red, C, out_dtype, epi, bias, mask, mask_dtype, colsum);
 }
 
 static int run_forward(rt_mlp* p, const rt_buf* x) {
@@ -201,6 +218,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     Ly.lbl_dw = "dw_l" + std::to_string(l);
     Ly.lbl_dw_red = "dw_reduce_l" + std::to_string(l);
     Ly.lbl_dx = "dx_l" + std::to_string(l);
+    Ly.lbl_bwd = "dwdx_l" + std::to_string(l);
   }
   p->n_params = off;
 
@@ -271,12 +289,25 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     return hip_fail(c, e, "mlp init");
   }
 
+  // Hidden layers whose dW and dX fit the fused pair launch.
+  for (int l = 1; l < n_layers; ++l) {
+    Layer& Ly = p->L[l];
+    const int dt = p->mixed ? RT_BF16 : RT_F32;
+    const GemmDesc dw = plan_desc(p, RT_TN, dt, p->L[l - 1].act, Ly.delta, p->grad + Ly.w_off, RT_F32, (int)Ly.din,
+                                  (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr,
+                                  RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
+    const GemmDesc dx = plan_desc(p, RT_NT, dt, Ly.delta, p->theta + Ly.w_off, p->L[l - 1].delta, RT_F32, (int)batch,
+                                  (int)Ly.din, (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr,
+                                  p->L[l - 1].act, RT_F32, nullptr, 1);
+    Ly.pair_bwd = gemm_pair_supported(dw, dx);
+  }
+
   // Launch count of one step.
   int n = 0;
   for (int l = 0; l < n_layers; ++l) {
     n += p->L[l].splits_fwd > 1 ? 2 : 1;
     n += p->L[l].splits_dw > 1 ? 2 : 1;
-    if (l > 0) n += 1;
+    if (l > 0 && !p->L[l].pair_bwd) n += 1;
   }
   n += 1;  // softmax-xent
   n += 1;  // optimizer
@@ -338,20 +369,42 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
     const void* dl = p->mixed ? Ly.delta_h : (const void*)Ly.delta;
     // dW_l = A_{l-1}ᵀ·δ_l  (TN; A stored [batch, din]), db_l = 1ᵀ·δ_l fused.
-    rc = plan_gemm(p, Ly.lbl_dw.c_str(), Ly.lbl_dw_red.c_str(), RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32,
-                   (int)Ly.din, (int)Ly.dout, B, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32,
-                   p->grad + Ly.b_off, Ly.splits_dw);
-    if (rc) return rc;
-    if (l > 0) {
+    const GemmDesc dw = plan_desc(p, RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32, (int)Ly.din, (int)Ly.dout,
+                                  B, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32,
+                                  p->grad + Ly.b_off, Ly.splits_dw);
+    if (l == 0) {
+      {
+        Launch Lz(c, Ly.lbl_dw.c_str());
+        hipError_t e = gemm_launch(c->stream, dw);
+        if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
+      }
+    } else {
       Layer& Lp = p->L[l - 1];
       const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
       // δ_{l-1} = (δ_l·W_lᵀ) ⊙ 1[A_{l-1} > 0]  (NT; W stored [din, dout] = [N, K]).
       void* dst = p->mixed ? Lp.delta_h : (void*)Lp.delta;
-      rc = plan_gemm(p, Ly.lbl_dx.c_str(), "", RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B,
-                     (int)Ly.din, (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
-                     p->mixed ? RT_BF16 : RT_F32, nullptr, 1);
-      if (rc) return rc;
+      const GemmDesc dx = plan_desc(p, RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B, (int)Ly.din,
+                                    (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
+                                    p->mixed ? RT_BF16 : RT_F32, nullptr, 1);
+      if (Ly.pair_bwd) {
+        // Both read δ_l and neither feeds the other: one launch.
+        Launch Lz(c, Ly.lbl_bwd.c_str());
+        hipError_t e = gemm_pair_launch(c->stream, dw, dx);
+        if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_bwd.c_str());
+      } else {
+        {
+          Launch Lz(c, Ly.lbl_dw.c_str());
+          hipError_t e = gemm_launch(c->stream, dw);
+          if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
+        }
+        Launch Lz(c, Ly.lbl_dx.c_str());
+        hipError_t e = gemm_launch(c->stream, dx);
+        if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dx.c_str());
+      }
     }
+    rc = finish_split(p, dw, Ly.lbl_dw_red.c_str(), p->grad + Ly.w_off, RT_F32, RT_EPI_NONE, nullptr, nullptr, RT_F32,
+                      p->grad + Ly.b_off);
+    if (rc) return rc;
   }
 
   if (p->mixed) {

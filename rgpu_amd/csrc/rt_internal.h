@@ -89,6 +89,11 @@ struct GemmDesc {
 // Enqueues C (or its partial planes) on stream.  Shapes and pointers are
 // validated by the caller.
 hipError_t gemm_launch(hipStream_t s, const GemmDesc& d);
+// Two independent GEMMs in one launch: d0 TN (any K slices) and d1 NT
+// (whole K), f32, where both would run on 64x64 tiles.  gemm_pair_supported
+// says whether gemm_pair_launch accepts the pair.
+bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1);
+hipError_t gemm_pair_launch(hipStream_t s, const GemmDesc& d0, const GemmDesc& d1);
 // Sums `splits` f32 partial planes of [M, N] in slice order into C and applies
 // the epilogue; also sums colsum partials [splits, N] into colsum if given.
 hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M,
