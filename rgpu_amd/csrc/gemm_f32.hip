@@ -41,8 +41,6 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 
-constexpr int kThreads = 256;
-
 struct F32Args {
   const float* A;
   const float* B;
@@ -91,24 +89,40 @@ __device__ inline f4 load4(const float* base, int ld, int row, int col, int rows
 }
 
 // One block's work: tile `bid` (already XCD-renumbered, in [0, tiles)) of
-// K slice `split`.  smem holds the two LDS stages of both operands.
-template <int BM, int BN, bool A_KC, bool B_KC>
+// K slice `split`.
+//
+// The block is KS groups of 2x2 waves.  Every group computes the whole
+// BM x BN tile, each over its own share of every BK-wide K step (SUB
+// sub-steps of 16), and at the end the groups' accumulators are summed
+// through LDS in group order.  More waves per tile hide more load latency
+// without shrinking the tile.  PF is how many K steps ahead the global loads
+// run: 1 (one register stage) or 2 (two register stages, alternating).
+template <int BM, int BN, bool A_KC, bool B_KC, int BK = 32, int KS = 1, int PF = 1>
 struct F32Tile {
-  static constexpr int BK = 32, PAD = 4;
+  static constexpr int THREADS = 256 * KS;
+  static constexpr int PAD = 4;
   static constexpr int TM = BM / 32, TN = BN / 32;  // MFMA tiles per wave (2x2 waves of BM/2 x BN/2)
   static constexpr int A_STRIDE = A_KC ? (BK + PAD) : (BM + PAD);
   static constexpr int B_STRIDE = B_KC ? (BK + PAD) : (BN + PAD);
   static constexpr int A_ELEMS = A_KC ? BM * A_STRIDE : BK * A_STRIDE;
   static constexpr int B_ELEMS = B_KC ? BN * B_STRIDE : BK * B_STRIDE;
-  static constexpr int SMEM = 2 * (A_ELEMS + B_ELEMS);  // floats
-  static constexpr int A_LD = BM / 32, B_LD = BN / 32;  // float4 loads per thread per K step
+  static constexpr int PIPE = 2 * (A_ELEMS + B_ELEMS);  // floats: two stages of both operands
+  static constexpr int RED = (KS - 1) * BM * BN;        // floats: accumulators of groups 1..KS-1
+  static constexpr int SMEM = PIPE > RED ? PIPE : RED;
+  static constexpr int A_LD = BM * BK / 4 / THREADS;  // float4 loads per thread per K step
+  static constexpr int B_LD = BN * BK / 4 / THREADS;
+  static constexpr int SUB = BK / 16 / KS;
   static_assert(BM % 32 == 0 && BN % 32 == 0 && BM <= 128 && BN <= 128, "tile");
+  static_assert(A_LD >= 1 && B_LD >= 1 && BM * BK % (4 * THREADS) == 0 && BN * BK % (4 * THREADS) == 0,
+                "tile loads must split evenly over the threads");
+  static_assert(SUB >= 1 && BK % (16 * KS) == 0, "each group takes whole 16-wide sub-steps");
+  static_assert(PF == 1 || PF == 2, "prefetch depth");
 
   __device__ static void run(const F32Args& p, int bid, int split, float* smem);
 };
 
-template <int BM, int BN, bool A_KC, bool B_KC>
-__device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int split, float* smem) {
+template <int BM, int BN, bool A_KC, bool B_KC, int BK, int KS, int PF>
+__device__ void F32Tile<BM, BN, A_KC, B_KC, BK, KS, PF>::run(const F32Args& p, int bid, int split, float* smem) {
   float* const sA0 = smem;
   float* const sB0 = smem + 2 * A_ELEMS;
   auto sA = [&](int buf) { return sA0 + buf * A_ELEMS; };
@@ -116,8 +130,9 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  const int kg = wave >> 2, wq = wave & 3;  // K group, wave within the group
   const int g = lane >> 4, r = lane & 15;
-  const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  const int wm = (wq >> 1) * (BM / 2), wn = (wq & 1) * (BN / 2);
 
   constexpr int GROUP = 8;
   const int per_group = GROUP * p.tiles_n;
@@ -133,14 +148,12 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
   const int ke = min(p.K, kb + p.k_per_split);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
 
-  f4 ra[A_LD], rb[B_LD];
-
-  auto load_tiles = [&](int k0) {
+  auto load_tiles = [&](f4 (&ra)[A_LD], f4 (&rb)[B_LD], int k0) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-      const int idx = tid + kThreads * i;
+      const int idx = tid + THREADS * i;
       if constexpr (A_KC) {
-        const int rr = idx >> 3, kq = idx & 7;  // 8 float4 per 32-wide K row
+        const int rr = idx / (BK / 4), kq = idx % (BK / 4);
         ra[i] = load4(p.A, p.lda, m0 + rr, k0 + 4 * kq, p.M, ke, p.vec_a);
       } else {
         constexpr int Q = BM / 4;
@@ -150,9 +163,9 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-      const int idx = tid + kThreads * i;
+      const int idx = tid + THREADS * i;
       if constexpr (B_KC) {
-        const int rr = idx >> 3, kq = idx & 7;
+        const int rr = idx / (BK / 4), kq = idx % (BK / 4);
         rb[i] = load4(p.B, p.ldb, n0 + rr, k0 + 4 * kq, p.N, ke, p.vec_b);
       } else {
         constexpr int Q = BN / 4;
@@ -161,12 +174,12 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
       }
     }
   };
-  auto store_tiles = [&](int buf) {
+  auto store_tiles = [&](const f4 (&ra)[A_LD], const f4 (&rb)[B_LD], int buf) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-      const int idx = tid + kThreads * i;
+      const int idx = tid + THREADS * i;
       if constexpr (A_KC) {
-        *reinterpret_cast<f4*>(&sA(buf)[(idx >> 3) * A_STRIDE + 4 * (idx & 7)]) = ra[i];
+        *reinterpret_cast<f4*>(&sA(buf)[(idx / (BK / 4)) * A_STRIDE + 4 * (idx % (BK / 4))]) = ra[i];
       } else {
         constexpr int Q = BM / 4;
         *reinterpret_cast<f4*>(&sA(buf)[(idx / Q) * A_STRIDE + 4 * (idx % Q)]) = ra[i];
@@ -174,9 +187,9 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
     }
 #pragma unroll
     for (int i = 0; i < B_LD; ++i) {
-      const int idx = tid + kThreads * i;
+      const int idx = tid + THREADS * i;
       if constexpr (B_KC) {
-        *reinterpret_cast<f4*>(&sB(buf)[(idx >> 3) * B_STRIDE + 4 * (idx & 7)]) = rb[i];
+        *reinterpret_cast<f4*>(&sB(buf)[(idx / (BK / 4)) * B_STRIDE + 4 * (idx % (BK / 4))]) = rb[i];
       } else {
         constexpr int Q = BN / 4;
         *reinterpret_cast<f4*>(&sB(buf)[(idx / Q) * B_STRIDE + 4 * (idx % Q)]) = rb[i];
@@ -194,7 +207,8 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
     const float* as = sA(buf);
     const float* bs = sB(buf);
 #pragma unroll
-    for (int ss = 0; ss < BK / 16; ++ss) {
+    for (int s2 = 0; s2 < SUB; ++s2) {
+      const int ss = kg * SUB + s2;
       float af[TM][4], bf[TN][4];
       if constexpr (A_KC) {
 #pragma unroll
@@ -234,28 +248,81 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
   // the first M tile's blocks, summed over k in increasing order.
   const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0 && tid < BN;
   float cs = 0.0f;
+  auto colsum = [&](int buf) {
+    if constexpr (!B_KC) {
+      if (do_cs) {
+        const float* bs = sB(buf);
+#pragma unroll 8
+        for (int kk = 0; kk < BK; ++kk) cs += bs[kk * B_STRIDE + tid];
+      }
+    }
+  };
 
   if (nk > 0) {
-    load_tiles(kb);
-    store_tiles(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < nk) load_tiles(kb + (kt + 1) * BK);
-      compute(cur);
-      if constexpr (!B_KC) {
-        if (do_cs) {
-          const float* bs = sB(cur);
-#pragma unroll 8
-          for (int kk = 0; kk < BK; ++kk) cs += bs[kk * B_STRIDE + tid];
-        }
-      }
-      if (kt + 1 < nk) store_tiles(cur ^ 1);
+    if constexpr (PF == 1) {
+      f4 ra[A_LD], rb[B_LD];
+      load_tiles(ra, rb, kb);
+      store_tiles(ra, rb, 0);
       __syncthreads();
+      for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) load_tiles(ra, rb, kb + (kt + 1) * BK);
+        compute(cur);
+        colsum(cur);
+        if (kt + 1 < nk) store_tiles(ra, rb, cur ^ 1);
+        __syncthreads();
+      }
+    } else {
+      // Register stage j holds K step kt + j; the loads of step kt + 2 are
+      // issued before step kt computes and stored after step kt + 1 does.
+      f4 ra0[A_LD], rb0[B_LD], ra1[A_LD], rb1[B_LD];
+      load_tiles(ra0, rb0, kb);
+      if (nk > 1) load_tiles(ra1, rb1, kb + BK);
+      store_tiles(ra0, rb0, 0);
+      __syncthreads();
+      auto iter = [&](int kt, f4 (&la)[A_LD], f4 (&lb)[B_LD], const f4 (&sa)[A_LD], const f4 (&sb)[B_LD]) {
+        const int cur = kt & 1;
+        if (kt + 2 < nk) load_tiles(la, lb, kb + (kt + 2) * BK);
+        compute(cur);
+        colsum(cur);
+        if (kt + 1 < nk) store_tiles(sa, sb, cur ^ 1);
+        __syncthreads();
+      };
+      for (int kt = 0; kt < nk; kt += 2) {
+        iter(kt, ra0, rb0, ra1, rb1);
+        if (kt + 1 < nk) iter(kt + 1, ra1, rb1, ra0, rb0);
+      }
     }
   }
 
   if (do_cs && n0 + tid < p.N) p.colsum[(long long)split * p.N + n0 + tid] = cs;
+
+  if constexpr (KS > 1) {
+    // Groups 1.. park their accumulators (the main loop ended on a barrier,
+    // so the pipeline buffers are free); group 0 adds them in group order.
+    constexpr int PER = TM * TN * 4;
+    if (kg > 0) {
+      float* dst = smem + ((kg - 1) * 4 + wq) * PER * 64 + lane;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dst[((t * TN + u) * 4 + q) * 64] = acc[t][u][q];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int j = 1; j < KS; ++j) {
+      const float* src = smem + ((j - 1) * 4 + wq) * PER * 64 + lane;
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[t][u][q] += src[((t * TN + u) * 4 + q) * 64];
+    }
+  }
 
   // Epilogue.  Lane owns rows m0+wm+TM*(4g+q)+t and columns n0+wn+TN*r+u.
   const bool partial = p.splits > 1;
@@ -303,9 +370,8 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC>::run(const F32Args& p, int bid, int 
   }
 }
 
-template <int BM, int BN, bool A_KC, bool B_KC>
-__global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
-  using T = F32Tile<BM, BN, A_KC, B_KC>;
+template <class T>
+__global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(F32Args p) {
   __shared__ __attribute__((aligned(16))) float smem[T::SMEM];
   T::run(p, xcd_local(blockIdx.x, gridDim.x), blockIdx.z, smem);
 }
@@ -315,7 +381,8 @@ __global__ __launch_bounds__(kThreads) void gemm_f32_kernel(F32Args p) {
 // folded into its block range.  n0 is a multiple of 8 so both problems are
 // spread evenly over the XCDs; problem 0 is dispatched first.
 template <class T0, class T1>
-__global__ __launch_bounds__(kThreads) void gemm_f32_pair_kernel(F32Args p0, F32Args p1, int n0) {
+__global__ __launch_bounds__(T0::THREADS) void gemm_f32_pair_kernel(F32Args p0, F32Args p1, int n0) {
+  static_assert(T0::THREADS == T1::THREADS, "one block size");
   constexpr int S = T0::SMEM > T1::SMEM ? T0::SMEM : T1::SMEM;
   __shared__ __attribute__((aligned(16))) float smem[S];
   const int b = blockIdx.x;
@@ -360,12 +427,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-template <int BM, int BN, bool A_KC, bool B_KC>
+template <int BM, int BN, bool A_KC, bool B_KC, int BK = 32, int KS = 1, int PF = 1>
 hipError_t launch_f32(hipStream_t s, F32Args a) {
+  using T = F32Tile<BM, BN, A_KC, B_KC, BK, KS, PF>;
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   dim3 grid(a.tiles_m * a.tiles_n, 1, a.splits);
-  hipLaunchKernelGGL((gemm_f32_kernel<BM, BN, A_KC, B_KC>), grid, dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((gemm_f32_kernel<T>), grid, dim3(T::THREADS), 0, s, a);
   return hipGetLastError();
 }
 
@@ -432,8 +500,8 @@ hipError_t launch_pair_tn_nt(hipStream_t s, F32Args a0, F32Args a1) {
   const long long nb1 = (long long)a1.tiles_m * a1.tiles_n * a1.splits;
   const long long n0 = (nb0 + 7) / 8 * 8;
   if (n0 + nb1 > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_f32_pair_kernel<T0, T1>), dim3((unsigned)(n0 + nb1)), dim3(kThreads), 0, s, a0, a1,
-                     (int)n0);
+  hipLaunchKernelGGL((gemm_f32_pair_kernel<T0, T1>), dim3((unsigned)(n0 + nb1)), dim3(T0::THREADS), 0, s, a0,
+                     a1, (int)n0);
   return hipGetLastError();
 }
 

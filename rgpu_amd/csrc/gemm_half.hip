@@ -170,6 +170,79 @@ struct Operand {
   }
 };
 
+// Epilogue through LDS, one 16-row slab of the wave tile at a time: the
+// accumulators acc[t][u][q] = C(m0+wm+16t+4g+q, n0+wn+16u+r) are parked in
+// a per-wave [16][WN+4] f32 region of smem, then each lane reads 4
+// consecutive columns back, applies bias / ReLU / mask and stores 16 (f32) or
+// 8 (bf16) bytes.  Bounded register use and coalesced stores.  The caller has
+// finished every read of smem (barrier) before calling.
+template <int BM, int BN, int WGM, int WGN, int SMEM_BYTES, int TM, int TN>
+__device__ __forceinline__ void store_tile(const HalfArgs& p, f4 (&acc)[TM][TN], unsigned short* smem, int m0, int n0,
+                                           int wm, int wn, int wave, int lane, int g, int r) {
+  constexpr int WN = BN / WGN;
+  constexpr int SROW = WN + 4;
+  static_assert(16 * SROW * 4 * WGM * WGN <= SMEM_BYTES, "epilogue staging must fit in LDS");
+  float* stage = reinterpret_cast<float*>(smem) + wave * 16 * SROW;
+  const bool partial = gridDim.z > 1;
+  const bool out_bf16 = !partial && p.out_bf16;
+  const bool vec_c = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
+  float* Cf = static_cast<float*>(p.C) + (partial ? (long long)blockIdx.z * p.split_stride : 0);
+  unsigned short* Ch = static_cast<unsigned short*>(p.C);
+  static_for<0, TM>([&](auto tc) {
+    constexpr int t = decltype(tc)::value;
+#pragma unroll
+    for (int u = 0; u < TN; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) stage[(4 * g + q) * SROW + 16 * u + r] = acc[t][u][q];
+    __syncthreads();
+    constexpr int C4 = WN / 4;  // float4 columns per slab row
+#pragma unroll
+    for (int j = 0; j < 16 * C4 / 64; ++j) {
+      const int idx = lane + 64 * j;
+      const int rr = idx / C4, c4 = idx % C4;
+      const int row = m0 + wm + 16 * t + rr;
+      const int col = n0 + wn + 4 * c4;
+      if (row >= p.M || col >= p.N) continue;
+      f4 v = *reinterpret_cast<const f4*>(&stage[rr * SROW + 4 * c4]);
+      const long long off = (long long)row * p.ldc + col;
+      const int nv = min(4, p.N - col);
+      if (!partial) {
+        if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (e < nv) v[e] = v[e] + p.bias[col + e];
+            if (p.epi == RT_EPI_BIAS_RELU) v[e] = fmaxf(v[e], 0.0f);
+          }
+        } else if (p.epi == RT_EPI_RELU_MASK) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (e < nv) {
+              const float mv = p.mask_bf16 ? bf16_to_f32(static_cast<const unsigned short*>(p.mask)[off + e])
+                                           : static_cast<const float*>(p.mask)[off + e];
+              if (!(mv > 0.0f)) v[e] = 0.0f;
+            }
+          }
+        }
+      }
+      if (out_bf16) {
+        if (vec_c && nv == 4) {
+          u2 w;
+          w[0] = (unsigned)f32_to_bf16_rne(v[0]) | ((unsigned)f32_to_bf16_rne(v[1]) << 16);
+          w[1] = (unsigned)f32_to_bf16_rne(v[2]) | ((unsigned)f32_to_bf16_rne(v[3]) << 16);
+          *reinterpret_cast<u2*>(&Ch[off]) = w;
+        } else {
+          for (int e = 0; e < nv; ++e) Ch[off + e] = f32_to_bf16_rne(v[e]);
+        }
+      } else {
+        if (vec_c && nv == 4) *reinterpret_cast<f4*>(&Cf[off]) = v;
+        else
+          for (int e = 0; e < nv; ++e) Cf[off + e] = v[e];
+      }
+    }
+    __syncthreads();
+  });
+}
+
 template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC, bool IS_BF16>
 __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_kernel(HalfArgs p) {
   constexpr int THREADS = 64 * WGM * WGN;
@@ -285,81 +358,420 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_kernel(HalfArgs p) {
     }
   }
 
-  // Epilogue through LDS, one 16-row slab of the wave tile at a time: the
-  // accumulators acc[t][u][q] = C(m0+wm+16t+4g+q, n0+wn+16u+r) are parked in
-  // a per-wave [16][WN+4] f32 region, then each lane reads 4 consecutive
-  // columns back, applies bias / ReLU / mask and stores 16 (f32) or 8 (bf16)
-  // bytes.  Bounded register use and coalesced stores.
-  constexpr int SROW = WN + 4;
-  static_assert(16 * SROW * 4 * WGM * WGN <= (int)sizeof(smem), "epilogue staging must fit in LDS");
-  float* stage = reinterpret_cast<float*>(smem) + wave * 16 * SROW;
-  const bool partial = gridDim.z > 1;
-  const bool out_bf16 = !partial && p.out_bf16;
-  const bool vec_c = (p.ldc % 4 == 0) && ((reinterpret_cast<uintptr_t>(p.C) & 15) == 0);
-  float* Cf = static_cast<float*>(p.C) + (partial ? (long long)blockIdx.z * p.split_stride : 0);
-  unsigned short* Ch = static_cast<unsigned short*>(p.C);
   __syncthreads();  // main-loop LDS reads are finished
-  static_for<0, TM>([&](auto tc) {
-    constexpr int t = decltype(tc)::value;
+  store_tile<BM, BN, WGM, WGN, (int)sizeof(smem)>(p, acc, smem, m0, n0, wm, wn, wave, lane, g, r);
+}
+
+
+// ---------------------------------------------------------------- full-tile kernel
+// For full tiles (M % BM == 0, N % BN == 0, every K slice a whole number of
+// BK steps, 16-byte aligned operands whose leading dimensions are multiples
+// of 8 halves) the operand tiles go from global memory straight into LDS
+// with global_load_lds_dwordx4: lane l's 16 bytes land at the instruction's
+// LDS base + 16 l, so a wave fills 1 KB of LDS per instruction with no VGPR
+// staging and no LDS write instructions, and the loads of stage k+1 run
+// while stage k computes.  Each lane picks the global chunk whose swizzled
+// LDS position is 16 l.  Layouts (unpadded):
+//   K-contiguous [row][64]: 16-byte granule j of row r at j ^ ((r >> 1) & 7)
+//     (b128 fragment reads of 16 rows at one granule are conflict-free);
+//   M/N-contiguous [k][ROWS]: 32-byte granule G of row k at G ^ hm(k).  A
+//     transposed fragment read touches, per 32 lanes, rows k0 + {0..3, 8..11}
+//     at one granule; hm gives those eight rows distinct bank groups.
+template <int ROWS, bool KC, int THREADS, int BKD>
+struct DmaOperand {
+  static constexpr int ELEMS = ROWS * BKD;    // halves per stage
+  static constexpr int INSTR = ELEMS / 512;   // 1 KB DMA instructions per stage
+  static constexpr int WAVES = THREADS / 64;
+  static constexpr int PER_WAVE = INSTR / WAVES;
+  static constexpr int GR = BKD / 8;          // 16-byte granules per K-contiguous row
+  static_assert(INSTR % WAVES == 0 && PER_WAVE >= 1, "DMA instructions must split evenly over the waves");
+  static_assert(ROWS % 64 == 0 && (BKD == 32 || BKD == 64), "tile shape");
+
+  // Wave w's i-th DMA instruction fills LDS block i * WAVES + w, so a lane's
+  // rows advance by RSTEP per instruction; with that spacing the swizzle term
+  // of a lane's chunk is the same for every instruction (or, for 256-wide
+  // M/N-contiguous tiles, alternates with the instruction's parity), and the
+  // rest of the offset is uniform: it goes in the scalar offset.
+  static constexpr int RSTEP = (KC ? 512 / BKD : 512 / ROWS) * WAVES;
+  static constexpr bool PAR = !KC && (RSTEP % 16) == 8;  // hm(k + RSTEP) != hm(k)
+
+  // Buffer descriptor based at the tile origin; this lane's byte offset from
+  // it for its first instruction (voff[1]: the odd instructions when PAR).
+  __amdgpu_buffer_rsrc_t rsrc;
+  int voff[2];
+  int row_bytes;  // bytes per stored row of the operand (2 ld)
+
+  // K-contiguous: granule j of row r is stored at j ^ kc_sw(r).  16 lanes read
+  // 16 consecutive rows at one granule; with 128-byte rows (BKD 64) two rows
+  // share a 256-byte bank line, with 64-byte rows four do.
+  __device__ static inline int kc_sw(int row) {
+    if constexpr (BKD == 64) return (row >> 1) & 7;
+    else return (row >> 2) & 3;
+  }
+  __device__ static inline int hm(int k) {
+    if constexpr (ROWS >= 128) return (k & 3) | (((k >> 3) & 1) << 2);
+    else return ((k >> 1) & 1) | (((k >> 3) & 1) << 1);
+  }
+  __device__ inline void init(const unsigned short* tile, int ld, int wave, int lane) {
+    static_assert(KC ? (RSTEP % 16 == 0) : (RSTEP % 8 == 0), "swizzle period");
+    // 0x00020000: raw (untyped) buffer, 32-bit data format.  The host only
+    // takes this path when every operand byte lies below 2^31 of its base.
+    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(tile), (short)0, 0x7fffffff, 0x00020000);
+    row_bytes = 2 * ld;
 #pragma unroll
-    for (int u = 0; u < TN; ++u)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) stage[(4 * g + q) * SROW + 16 * u + r] = acc[t][u][q];
-    __syncthreads();
-    constexpr int C4 = WN / 4;  // float4 columns per slab row
-#pragma unroll
-    for (int j = 0; j < 16 * C4 / 64; ++j) {
-      const int idx = lane + 64 * j;
-      const int rr = idx / C4, c4 = idx % C4;
-      const int row = m0 + wm + 16 * t + rr;
-      const int col = n0 + wn + 4 * c4;
-      if (row >= p.M || col >= p.N) continue;
-      f4 v = *reinterpret_cast<const f4*>(&stage[rr * SROW + 4 * c4]);
-      const long long off = (long long)row * p.ldc + col;
-      const int nv = min(4, p.N - col);
-      if (!partial) {
-        if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (e < nv) v[e] = v[e] + p.bias[col + e];
-            if (p.epi == RT_EPI_BIAS_RELU) v[e] = fmaxf(v[e], 0.0f);
-          }
-        } else if (p.epi == RT_EPI_RELU_MASK) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (e < nv) {
-              const float mv = p.mask_bf16 ? bf16_to_f32(static_cast<const unsigned short*>(p.mask)[off + e])
-                                           : static_cast<const float*>(p.mask)[off + e];
-              if (!(mv > 0.0f)) v[e] = 0.0f;
-            }
-          }
-        }
-      }
-      if (out_bf16) {
-        if (vec_c && nv == 4) {
-          u2 w;
-          w[0] = (unsigned)f32_to_bf16_rne(v[0]) | ((unsigned)f32_to_bf16_rne(v[1]) << 16);
-          w[1] = (unsigned)f32_to_bf16_rne(v[2]) | ((unsigned)f32_to_bf16_rne(v[3]) << 16);
-          *reinterpret_cast<u2*>(&Ch[off]) = w;
-        } else {
-          for (int e = 0; e < nv; ++e) Ch[off + e] = f32_to_bf16_rne(v[e]);
-        }
+    for (int par = 0; par < 2; ++par) {
+      if constexpr (KC) {
+        const int row = (512 / BKD) * wave + lane / GR, slot = lane % GR;
+        voff[par] = 2 * (row * ld + 8 * (slot ^ kc_sw(row)));
       } else {
-        if (vec_c && nv == 4) *reinterpret_cast<f4*>(&Cf[off]) = v;
-        else
-          for (int e = 0; e < nv; ++e) Cf[off + e] = v[e];
+        constexpr int CH = ROWS / 8;  // 16-byte chunks per LDS row
+        const int k = (512 / ROWS) * wave + lane / CH, s = lane % CH;
+        voff[par] = 2 * (k * ld + 16 * ((s >> 1) ^ hm(k + par * RSTEP)) + 8 * (s & 1));
       }
     }
+  }
+  // This wave's DMA of the stage `stage_bytes` past the tile origin into `lds`.
+  // The scalar offset is made opaque to the optimiser, which would otherwise
+  // fold each instruction's uniform part into a separate VGPR offset.
+  __device__ inline void issue(int stage_bytes, unsigned short* lds, int wave) const {
+#pragma unroll
+    for (int i = 0; i < PER_WAVE; ++i) {
+      int so = __builtin_amdgcn_readfirstlane(stage_bytes + i * RSTEP * row_bytes);
+      asm volatile("" : "+s"(so));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc,
+                                               (__attribute__((address_space(3))) void*)(lds + 512 * (i * WAVES + wave)),
+                                               16, voff[PAR ? (i & 1) : 0], so, 0, 0);
+    }
+  }
+  // Same fragment contract as Operand::frag.
+  __device__ inline u4 frag(const unsigned short* lds, int kk, int rbase, int g, int r) const {
+    if constexpr (KC) {
+      const int row = rbase + r;
+      return *reinterpret_cast<const u4*>(&lds[row * BKD + 8 * ((4 * kk + g) ^ kc_sw(row))]);
+    } else {
+      const int k = 32 * kk + 8 * g + (r >> 2);  // hm(k + 4) == hm(k)
+      const unsigned short* q = &lds[k * ROWS + 16 * ((rbase >> 4) ^ hm(k)) + 4 * (r & 3)];
+      const u2 lo = lds_tr(q), hi = lds_tr(q + 4 * ROWS);
+      return u4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  }
+  // 8 consecutive halves [c8*8, c8*8+8) of LDS row k (M/N-contiguous tiles).
+  __device__ static inline u4 row_chunk(const unsigned short* lds, int k, int c8) {
+    return *reinterpret_cast<const u4*>(&lds[k * ROWS + 16 * ((c8 >> 1) ^ hm(k)) + 8 * (c8 & 1)]);
+  }
+};
+
+// Workgroup barrier for the DMA pipeline: this wave's LDS reads are complete
+// (lgkmcnt 0), then s_barrier.  Unlike __syncthreads it does not wait for
+// outstanding global loads (the later stages in flight); the asm's memory
+// clobber keeps the compiler from moving LDS accesses across it.
+__device__ inline void barrier_lds() {
+  __builtin_amdgcn_s_waitcnt((0xF) | (0x3 << 14) | (0x7 << 4));  // lgkmcnt(0) only
+  asm volatile("s_barrier" ::: "memory");
+}
+
+// s_waitcnt vmcnt(N), leaving the LDS and export counters alone.
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Full-tile epilogue straight from the accumulators.  The DMA kernel issues
+// its MFMAs with the operands swapped (D = op(B)·op(A)), so lane (g, r) holds
+// C(m0+wm+16t+r, n0+wn+16u+4g+q) for q = 0..3: four consecutive columns of
+// one row.  Each 16x16 tile is then one 16-byte (f32) or 8-byte (bf16) store,
+// with the bias / mask read the same way; no LDS round trip and no bounds
+// checks (the host only takes this path for whole, aligned tiles).
+template <int EPI, bool OUT_BF16, int TM, int TN>
+__device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[TM][TN], int m0, int n0, int wm,
+                                             int wn, int g, int r) {
+  float* Cf = static_cast<float*>(p.C) + (gridDim.z > 1 ? (long long)blockIdx.z * p.split_stride : 0);
+  unsigned short* Ch = static_cast<unsigned short*>(p.C);
+#pragma unroll
+  for (int t = 0; t < TM; ++t) {
+    const long long row_off = (long long)(m0 + wm + 16 * t + r) * p.ldc;
+#pragma unroll
+    for (int u = 0; u < TN; ++u) {
+      const int col = n0 + wn + 16 * u + 4 * g;
+      const long long off = row_off + col;
+      f4 v = acc[t][u];
+      if constexpr (EPI == RT_EPI_BIAS || EPI == RT_EPI_BIAS_RELU) {
+        const f4 b = *reinterpret_cast<const f4*>(p.bias + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = v[e] + b[e];
+          if constexpr (EPI == RT_EPI_BIAS_RELU) v[e] = fmaxf(v[e], 0.0f);
+        }
+      } else if constexpr (EPI == RT_EPI_RELU_MASK) {
+        f4 mk;
+        if (p.mask_bf16) {
+          const u2 h = *reinterpret_cast<const u2*>(static_cast<const unsigned short*>(p.mask) + off);
+          mk = f4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
+                  __uint_as_float(h[1] & 0xffff0000u)};
+        } else {
+          mk = *reinterpret_cast<const f4*>(static_cast<const float*>(p.mask) + off);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (!(mk[e] > 0.0f)) v[e] = 0.0f;
+      }
+      if constexpr (OUT_BF16) {
+        u2 w;
+        w[0] = (unsigned)f32_to_bf16_rne(v[0]) | ((unsigned)f32_to_bf16_rne(v[1]) << 16);
+        w[1] = (unsigned)f32_to_bf16_rne(v[2]) | ((unsigned)f32_to_bf16_rne(v[3]) << 16);
+        *reinterpret_cast<u2*>(Ch + off) = w;
+      } else {
+        *reinterpret_cast<f4*>(Cf + off) = v;
+      }
+    }
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void store_direct_any(const HalfArgs& p, const f4 (&acc)[TM][TN], int m0, int n0, int wm,
+                                                 int wn, int g, int r) {
+  if (gridDim.z > 1) return store_direct<RT_EPI_NONE, false>(p, acc, m0, n0, wm, wn, g, r);  // raw partial plane
+  const bool hb = p.out_bf16;
+  switch (p.epi) {
+    case RT_EPI_BIAS:
+      return hb ? store_direct<RT_EPI_BIAS, true>(p, acc, m0, n0, wm, wn, g, r)
+                : store_direct<RT_EPI_BIAS, false>(p, acc, m0, n0, wm, wn, g, r);
+    case RT_EPI_BIAS_RELU:
+      return hb ? store_direct<RT_EPI_BIAS_RELU, true>(p, acc, m0, n0, wm, wn, g, r)
+                : store_direct<RT_EPI_BIAS_RELU, false>(p, acc, m0, n0, wm, wn, g, r);
+    case RT_EPI_RELU_MASK:
+      return hb ? store_direct<RT_EPI_RELU_MASK, true>(p, acc, m0, n0, wm, wn, g, r)
+                : store_direct<RT_EPI_RELU_MASK, false>(p, acc, m0, n0, wm, wn, g, r);
+    default:
+      return hb ? store_direct<RT_EPI_NONE, true>(p, acc, m0, n0, wm, wn, g, r)
+                : store_direct<RT_EPI_NONE, false>(p, acc, m0, n0, wm, wn, g, r);
+  }
+}
+
+// Two LDS stages of BKD = 64 k (two MFMA k-steps, kk = 0, 1).  With the
+// fragments of (stage k, kk 0) already in registers, stage k runs as
+//   A: read (k, kk 1) fragments       | MFMAs of (k, kk 0)
+//   B: wait for stage k+1, barrier, DMA stage k+2 into stage k's buffer,
+//      read (k+1, kk 0) fragments     | MFMAs of (k, kk 1)
+// so every LDS read overlaps MFMAs and there is one barrier per 64 k.  The
+// reads and the DMA are interleaved one per MFMA: a single wave per SIMD
+// never stalls on a full memory queue with MFMAs still to issue.
+template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC, bool IS_BF16, int BKD, int NS>
+__global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs p) {
+  constexpr int THREADS = 64 * WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int TM = WM / 16, TN = WN / 16;
+  using OpA = DmaOperand<BM, A_KC, THREADS, BKD>;
+  using OpB = DmaOperand<BN, B_KC, THREADS, BKD>;
+  constexpr int STAGE = OpA::ELEMS + OpB::ELEMS;
+  constexpr int PER_STAGE = OpA::PER_WAVE + OpB::PER_WAVE;  // DMA instructions per wave per stage
+  static_assert(BKD == 64 && NS == 2, "two stages of two MFMA k-steps");
+  __shared__ __attribute__((aligned(16))) unsigned short smem[NS * STAGE];
+  auto sA = [&](int buf) { return smem + buf * STAGE; };
+  auto sB = [&](int buf) { return smem + buf * STAGE + OpA::ELEMS; };
+
+  const int tid = threadIdx.x;
+  // Wave index as a scalar: the DMA's LDS destinations (M0) are then SALU
+  // arithmetic instead of per-instruction VGPRs kept live across the loop.
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
+
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * p.tiles_n;
+  const int grp = bid / per_group;
+  const int first_m = grp * GROUP;
+  const int gsize = min(p.tiles_m - first_m, GROUP);
+  const int in_grp = bid - grp * per_group;
+  const int tile_m = first_m + in_grp % gsize;
+  const int tile_n = in_grp / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const int kb = blockIdx.z * p.k_per_split;
+  const int nk = (min(p.K, kb + p.k_per_split) - kb) / BKD;  // whole stages (checked by the host)
+
+  OpA oa;
+  OpB ob;
+  oa.init(A_KC ? p.A + (long long)m0 * p.lda + kb : p.A + (long long)kb * p.lda + m0, p.lda, wave, lane);
+  ob.init(B_KC ? p.B + (long long)n0 * p.ldb + kb : p.B + (long long)kb * p.ldb + n0, p.ldb, wave, lane);
+  const int a_step = 2 * (A_KC ? BKD : BKD * p.lda);  // bytes per stage
+  const int b_step = 2 * (B_KC ? BKD : BKD * p.ldb);
+  auto issue = [&](int stage, int buf) {
+    oa.issue(stage * a_step, sA(buf), wave);
+    ob.issue(stage * b_step, sB(buf), wave);
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+#pragma unroll
+    for (int u = 0; u < TN; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto read_frags = [&](int buf, int kk, u4 (&fa)[TM], u4 (&fb)[TN]) {
+#pragma unroll
+    for (int u = 0; u < TN; ++u) fb[u] = ob.frag(sB(buf), kk, wn + 16 * u, g, r);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) fa[t] = oa.frag(sA(buf), kk, wm + 16 * t, g, r);
+  };
+  // Operands swapped: acc[t][u] accumulates the transposed 16x16 tile, so a
+  // lane ends up with four consecutive columns of one row (store_direct).
+  auto mfmas = [&](const u4 (&fa)[TM], const u4 (&fb)[TN]) {
+#pragma unroll
+    for (int t = 0; t < TM; ++t)
+#pragma unroll
+      for (int u = 0; u < TN; ++u) {
+        if constexpr (IS_BF16)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fb[u]),
+                                                              __builtin_bit_cast(bf16x8, fa[t]), acc[t][u], 0, 0, 0);
+        else
+          acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, fb[u]),
+                                                             __builtin_bit_cast(f16x8, fa[t]), acc[t][u], 0, 0, 0);
+      }
+  };
+  constexpr int N_DS = (A_KC ? TM : 2 * TM) + (B_KC ? TN : 2 * TN);  // LDS read instructions per k-step
+  constexpr int N_MF = TM * TN;
+  // Scheduling hint for the region just emitted: one MFMA, then one of the
+  // N_DS LDS reads, ...; one MFMA, then one of the N_VM DMA loads, ...; then
+  // the remaining MFMAs.  Small tiles are left to the scheduler.
+  auto interleave = [&](auto n_vm) {
+    constexpr int N_VM = decltype(n_vm)::value;
+    if constexpr (N_DS + N_VM <= N_MF) {
+      static_for<0, N_DS>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      });
+      static_for<0, N_VM>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one global (DMA) load
+      });
+      __builtin_amdgcn_sched_group_barrier(0x008, N_MF - N_DS - N_VM, 0);
+    }
+  };
+
+  // Column sums of the (M/N-contiguous) B tiles over k, first M tile only:
+  // thread t sums 8 consecutive columns (chunk t % (BN/8)) over the k rows
+  // t / (BN/8), t / (BN/8) + KG, ... of every stage; the KG partial rows are
+  // added in a fixed order at the end.
+  constexpr int CH = BN / 8, KG = THREADS / CH;
+  static_assert(B_KC || (THREADS % CH == 0 && BKD % KG == 0), "colsum split");
+  const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0;  // uniform over the block
+  float cs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto colsum = [&](int buf) {
+    if constexpr (!B_KC) {
+      if (do_cs) {
+        const int c8 = tid % CH;
+#pragma unroll
+        for (int k = tid / CH; k < BKD; k += KG) {
+          const u4 v = OpB::row_chunk(sB(buf), k, c8);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            cs[2 * d] += half_to_f32<IS_BF16>((unsigned short)(v[d] & 0xffffu));
+            cs[2 * d + 1] += half_to_f32<IS_BF16>((unsigned short)(v[d] >> 16));
+          }
+        }
+      }
+    }
+  };
+
+  if (nk > 0) {
+    u4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    // Every B step waits for everything and issues one stage of DMA (past
+    // the last stage it re-fetches stage nk-1 into a buffer nothing reads),
+    // so the bookkeeping is the same in every stage.
+    issue(0, 0);
+    issue(min(1, nk - 1), 1);
+    wait_vm<PER_STAGE>();
+    barrier_lds();
+    read_frags(0, 0, fa0, fb0);
+    auto stage = [&](int k, auto bc) {
+      constexpr int BUF = decltype(bc)::value;  // k % 2
+      // A: (k, kk 1) fragments in, (k, kk 0) MFMAs.
+      read_frags(BUF, 1, fa1, fb1);
+      mfmas(fa0, fb0);
+      interleave(std::integral_constant<int, 0>{});
+      colsum(BUF);
+      // B: stage k+1 everywhere; stage k no longer read.
+      wait_vm<0>();
+      barrier_lds();
+      issue(min(k + 2, nk - 1), BUF);
+      read_frags(BUF ^ 1, 0, fa0, fb0);  // (k+1, kk 0); discarded after the last stage
+      mfmas(fa1, fb1);
+      interleave(std::integral_constant<int, PER_STAGE>{});
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    for (int k = 0; k < nk; k += 2) {
+      stage(k, B0{});
+      if (k + 1 < nk) stage(k + 1, B1{});
+    }
+  }
+  __syncthreads();  // main-loop LDS reads are finished
+
+  if (do_cs) {
+    float* red = reinterpret_cast<float*>(smem);  // [KG][BN]
+    const int c8 = tid % CH, kg = tid / CH;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[kg * BN + 8 * c8 + e] = cs[e];
     __syncthreads();
-  });
+    for (int col = tid; col < BN; col += THREADS) {
+      float v = 0.0f;
+      for (int j = 0; j < KG; ++j) v += red[j * BN + col];
+      p.colsum[(long long)blockIdx.z * p.N + n0 + col] = v;
+    }
+  }
+
+  store_direct_any<TM, TN>(p, acc, m0, n0, wm, wn, g, r);
+}
+
+// Direct-to-LDS pipeline shape: K per stage and number of stages.
+constexpr int kDmaBK = 64, kDmaStages = 2;
+
+template <int BM, int BN>
+void set_tiles(HalfArgs& a) {
+  a.tiles_m = (a.M + BM - 1) / BM;
+  a.tiles_n = (a.N + BN - 1) / BN;
+}
+
+// Whole BM x BN tiles everywhere, every K slice (the last included) a
+// multiple of the DMA stage, and operands the DMA can read 16 bytes at a time.
+bool full_tiles(const HalfArgs& a, int splits, int BM, int BN) {
+  const int last = a.K - (splits - 1) * a.k_per_split;
+  auto al = [](const void* ptr, unsigned n) { return (reinterpret_cast<uintptr_t>(ptr) & (n - 1)) == 0; };
+  const bool bf16_out = splits == 1 && a.out_bf16;
+  const bool epi_ok = (a.epi != RT_EPI_BIAS && a.epi != RT_EPI_BIAS_RELU) || al(a.bias, 16);
+  const bool mask_ok = a.epi != RT_EPI_RELU_MASK || al(a.mask, a.mask_bf16 ? 8 : 16);
+  return a.M % BM == 0 && a.N % BN == 0 && a.k_per_split % kDmaBK == 0 && last > 0 && last % kDmaBK == 0 &&
+         a.vec_a && a.vec_b && a.ldc % 4 == 0 && al(a.C, bf16_out ? 8 : 16) && epi_ok && mask_ok;
+}
+
+// The DMA addresses operands through 32-bit byte offsets from a tile origin.
+template <bool A_KC, bool B_KC>
+bool dma_addressable(const HalfArgs& a) {
+  const long long lim = 1LL << 31;
+  return (long long)(A_KC ? a.M : a.K) * a.lda * 2 < lim && (long long)(B_KC ? a.N : a.K) * a.ldb * 2 < lim;
 }
 
 template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
-hipError_t launch_cfg(hipStream_t s, HalfArgs a, int splits, bool bf16) {
-  a.tiles_m = (a.M + BM - 1) / BM;
-  a.tiles_n = (a.N + BN - 1) / BN;
-  dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
-  dim3 block(64 * WGM * WGN);
+hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16) {
+  set_tiles<BM, BN>(a);
+  const dim3 grid(a.tiles_m * a.tiles_n, 1, splits), block(64 * WGM * WGN);
+  if (bf16)
+    hipLaunchKernelGGL((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true, kDmaBK, kDmaStages>), grid, block, 0,
+                       s, a);
+  else
+    hipLaunchKernelGGL((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false, kDmaBK, kDmaStages>), grid, block,
+                       0, s, a);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
+hipError_t launch_regs(hipStream_t s, HalfArgs a, int splits, bool bf16) {
+  set_tiles<BM, BN>(a);
+  const dim3 grid(a.tiles_m * a.tiles_n, 1, splits), block(64 * WGM * WGN);
   if (bf16)
     hipLaunchKernelGGL((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true>), grid, block, 0, s, a);
   else
@@ -369,15 +781,26 @@ hipError_t launch_cfg(hipStream_t s, HalfArgs a, int splits, bool bf16) {
 
 template <bool A_KC, bool B_KC>
 hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16) {
-  // 256x256 blocks of 8 waves (2 per SIMD, 64x128 wave tiles) when they give
-  // at least one block per CU -- the fastest measured shape for all three
-  // layouts at 8192x4096x4096; 128x128 (4 waves) for mid sizes; 64x64 for
-  // small ones.
+  // 256x256 blocks when they give at least one block per CU, 128x128 for mid
+  // sizes, 64x64 for small ones.  Full tiles take the direct-to-LDS kernel
+  // (256x256: one wave per SIMD with a 128x128 wave tile, the accumulators in
+  // AGPRs); the rest the register-staged kernel (256x256: two waves per SIMD
+  // with 64x128 wave tiles).
   const long long tbig = (long long)((a.M + 255) / 256) * ((a.N + 255) / 256) * splits;
   const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
-  if (tbig >= 256) return launch_cfg<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
-  if (t128 >= 128) return launch_cfg<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
-  return launch_cfg<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+  if (tbig >= 256) {
+    if (full_tiles(a, splits, 256, 256) && dma_addressable<A_KC, B_KC>(a))
+      return launch_dma<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
+    return launch_regs<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
+  }
+  if (t128 >= 128) {
+    if (full_tiles(a, splits, 128, 128) && dma_addressable<A_KC, B_KC>(a))
+      return launch_dma<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+    return launch_regs<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+  }
+  if (full_tiles(a, splits, 64, 64) && dma_addressable<A_KC, B_KC>(a))
+    return launch_dma<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+  return launch_regs<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
 }
 
 }  // namespace
