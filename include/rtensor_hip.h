@@ -193,6 +193,14 @@ int rt_profile_reset(rt_ctx* ctx);
 int rt_profile_report(rt_ctx* ctx, char* names, size_t name_len, int* counts, double* ms, int cap,
                       int* n_out);
 
+/* Region timer, a measurement helper with no counterpart in rtensor: HIP
+ * events recorded on the ctx stream around everything enqueued between the
+ * two calls (no per-launch events inside the region).  rt_timer_end blocks
+ * and returns the elapsed device milliseconds; RT_ERR_INVALID without a
+ * preceding rt_timer_begin. */
+int rt_timer_begin(rt_ctx* ctx);
+int rt_timer_end(rt_ctx* ctx, float* ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,9 @@ struct rt_ctx {
   std::vector<rt_mlp*> mlps;
   std::vector<rt_prof_rec> prof;
   std::vector<hipEvent_t> event_pool;
+  // Region timer (rt_timer_begin / rt_timer_end).
+  hipEvent_t timer0 = nullptr, timer1 = nullptr;
+  bool timer_running = false;
 };
 
 namespace rt {

@@ -161,6 +161,8 @@ int rt_close(rt_ctx* c) {
     hipEventDestroy(r.e1);
   }
   for (auto e : c->event_pool) hipEventDestroy(e);
+  if (c->timer0) hipEventDestroy(c->timer0);
+  if (c->timer1) hipEventDestroy(c->timer1);
   hipFree(c->d_flags);
   if (c->scratch) hipFree(c->scratch);
   hipStreamDestroy(c->stream);
@@ -648,6 +650,25 @@ int rt_profile_report(rt_ctx* c, char* names, size_t name_len, int* counts, doub
     ++n;
   }
   if (n_out) *n_out = n;
+  return RT_OK;
+}
+
+int rt_timer_begin(rt_ctx* c) {
+  CHECK_CTX(c);
+  if (!c->timer0) HIP_TRY(c, hipEventCreate(&c->timer0), "timer event");
+  if (!c->timer1) HIP_TRY(c, hipEventCreate(&c->timer1), "timer event");
+  HIP_TRY(c, hipEventRecord(c->timer0, c->stream), "timer begin");
+  c->timer_running = true;
+  return RT_OK;
+}
+
+int rt_timer_end(rt_ctx* c, float* ms) {
+  CHECK_CTX(c);
+  if (!c->timer_running || ms == nullptr) return fail(c, RT_ERR_INVALID, "rt_timer_end without rt_timer_begin");
+  c->timer_running = false;
+  HIP_TRY(c, hipEventRecord(c->timer1, c->stream), "timer end");
+  HIP_TRY(c, hipEventSynchronize(c->timer1), "timer sync");
+  HIP_TRY(c, hipEventElapsedTime(ms, c->timer0, c->timer1), "timer elapsed");
   return RT_OK;
 }
 

@@ -89,6 +89,8 @@ SIGNATURES = {
     "rt_profile_reset": (C.c_int, [_VP]),
     "rt_profile_report": (C.c_int, [_VP, C.c_char_p, C.c_size_t, C.POINTER(C.c_int), C.POINTER(C.c_double),
                                     C.c_int, C.POINTER(C.c_int)]),
+    "rt_timer_begin": (C.c_int, [_VP]),
+    "rt_timer_end": (C.c_int, [_VP, C.POINTER(C.c_float)]),
 }
 
 
@@ -312,6 +314,16 @@ class Gpu:
 
     def profile_reset(self) -> None:
         self._call("rt_profile_reset", self._h)
+
+    def timer_begin(self) -> None:
+        """Start a region timer: a HIP event on the library stream."""
+        self._call("rt_timer_begin", self._h)
+
+    def timer_end(self) -> float:
+        """Device milliseconds since timer_begin (blocks)."""
+        ms = C.c_float()
+        self._call("rt_timer_end", self._h, C.byref(ms))
+        return ms.value
 
     def perfilar(self) -> List[tuple]:
         """Per-label (name, launches, device ms) since the last reset (Gpu::perfilar, mod.rs:1245-1286)."""

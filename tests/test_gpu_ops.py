@@ -354,3 +354,17 @@ def test_half_gemm_large_tiles(gpu, m, n, k, dt):
     cs = gpu.zeros((1, n))
     gpu.gemm(G.TN, gpu.upload(a.T.copy(), dt), gpu.upload(b, dt), c, colsum=cs)
     assert O.erro_rel(br.sum(0, keepdims=True), gpu.download(cs)) < 1e-5
+
+
+@pytest.mark.gpu
+def test_region_timer(gpu):
+    a = gpu.upload(np.ones((256, 256), np.float32))
+    c = gpu.zeros((256, 256))
+    gpu.timer_begin()
+    for _ in range(3):
+        gpu.gemm(G.NN, a, a, c)
+    ms = gpu.timer_end()
+    assert 0.0 < ms < 1000.0
+    assert np.all(gpu.download(c) == 256.0)
+    with pytest.raises(G.RtError):
+        gpu.timer_end()  # no region open
