@@ -34,6 +34,7 @@
 // splitk_reduce sums the planes in slice order (REDUZ, splitk.rs:240-256):
 // deterministic, no float atomics.
 
+#include "device_util.h"
 #include "rt_internal.h"
 
 namespace {
@@ -370,6 +371,244 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC, BK, KS, PF>::run(const F32Args& p, i
   }
 }
 
+// ---------------------------------------------------------------- full-tile kernel
+// For whole 64x64 tiles with 16-byte aligned operands the tiles go from
+// global memory straight into LDS (buffer_load ... lds: lane l's 16 bytes
+// land at the instruction's LDS base + 16 l), two stages of BK = 32 k.
+// Within a stage the two 16-k halves are pipelined around one barrier:
+//   A: read (k, half 1) fragments     | MFMAs of (k, half 0)
+//   B: wait for stage k+1, barrier, DMA stage k+2 into stage k's buffer,
+//      read (k+1, half 0) fragments   | MFMAs of (k, half 1)
+// MFMAs take the operands swapped (D = op(B)·op(A)), so lane (g, r) ends with
+// C(m0+wm+16t+r, n0+wn+16u+4g+q), q = 0..3: one float4 store per 16x16 tile.
+//
+// LDS layouts (unpadded, bank-conflict-free for the fragment reads):
+//   K-contiguous [row][32]: 16-byte granule j of row r at j ^ ((r >> 1) & 7);
+//     a fragment is one b128 read of row 16t + r at granule 4 half + g (the
+//     four k of the lane's four MFMA steps);
+//   M/N-contiguous [k][64]: 64-byte chunk c of row k at c ^ ((k >> 2) & 3); a
+//     fragment is four b32 reads (k = 16 half + 4g + s, column 16u + r).
+struct F32Dma {
+  static constexpr int BM = 64, BN = 64, BK = 32, THREADS = 256, WAVES = 4;
+  static constexpr int TM = 2, TN = 2;                 // 16x16 MFMA tiles per wave (32x32 wave tile)
+  static constexpr int ELEMS = 64 * BK;                // floats per operand per stage
+  static constexpr int PER_WAVE = ELEMS / 256 / WAVES; // 1 KB DMA instructions per operand per wave
+  static constexpr int STAGE = 2 * ELEMS;
+  static constexpr int SMEM = 2 * STAGE;               // floats: two stages of both operands
+  static constexpr int PER_STAGE = 2 * PER_WAVE;
+
+  template <bool KC>
+  struct Op {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int voff;       // this lane's byte offset from the tile origin (first instruction)
+    int istep;      // bytes between a lane's consecutive instructions (uniform)
+    // Wave w's i-th instruction fills LDS floats [256 (4 i + w), +256); with
+    // that spacing the lane's swizzle term is the same for every instruction.
+    __device__ inline void init(const float* tile, int ld, int wave, int lane) {
+      rsrc = rt_dev::raw_rsrc(tile);
+      if constexpr (KC) {
+        const int row = 8 * wave + (lane >> 3), slot = lane & 7;  // 8 rows of 128 B per instruction
+        voff = 4 * (row * ld + 4 * (slot ^ ((row >> 1) & 7)));
+        istep = 4 * 32 * ld;                                        // 32 rows
+      } else {
+        const int k = 4 * wave + (lane >> 4), s = lane & 15;        // 4 rows of 256 B per instruction
+        voff = 4 * (k * ld + 16 * ((s >> 2) ^ ((k >> 2) & 3)) + 4 * (s & 3));
+        istep = 4 * 16 * ld;                                        // 16 rows
+      }
+    }
+    __device__ inline void issue(int stage_bytes, float* lds, int wave) const {
+#pragma unroll
+      for (int i = 0; i < PER_WAVE; ++i) rt_dev::dma16(rsrc, lds + 256 * (4 * i + wave), voff, stage_bytes + i * istep);
+    }
+    // Fragment of MFMA tile `base` (16 rows / columns) for k-half h: the
+    // lane's four k values 16 h + 4 g + s, s = 0..3.
+    __device__ static inline f4 frag(const float* lds, int h, int base, int g, int r) {
+      if constexpr (KC) {
+        const int row = base + r;
+        return *reinterpret_cast<const f4*>(&lds[row * BK + 4 * ((4 * h + g) ^ ((row >> 1) & 7))]);
+      } else {
+        const int col = base + r;
+        f4 v;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int k = 16 * h + 4 * g + s;  // (k >> 2) & 3 == g
+          v[s] = lds[k * BM + 16 * ((col >> 4) ^ g) + (col & 15)];
+        }
+        return v;
+      }
+    }
+    // Element (k, col) of an M/N-contiguous stage.
+    __device__ static inline float at(const float* lds, int k, int col) {
+      return lds[k * BM + 16 * ((col >> 4) ^ ((k >> 2) & 3)) + (col & 15)];
+    }
+  };
+
+  template <bool A_KC, bool B_KC>
+  __device__ static void run(const F32Args& p, int bid, int split, float* smem);
+};
+
+template <int EPI>
+__device__ __forceinline__ void f32_store_direct(const F32Args& p, const f4 (&acc)[2][2], int m0, int n0, int wm,
+                                                 int wn, int g, int r, int split) {
+  float* C = p.C + (p.splits > 1 ? (long long)split * p.split_stride : 0);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const long long row_off = (long long)(m0 + wm + 16 * t + r) * p.ldc;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int col = n0 + wn + 16 * u + 4 * g;
+      f4 v = acc[t][u];
+      if constexpr (EPI == RT_EPI_BIAS || EPI == RT_EPI_BIAS_RELU) {
+        const f4 b = *reinterpret_cast<const f4*>(p.bias + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = v[e] + b[e];
+          if constexpr (EPI == RT_EPI_BIAS_RELU) v[e] = fmaxf(v[e], 0.0f);
+        }
+      } else if constexpr (EPI == RT_EPI_RELU_MASK) {
+        const f4 mk = *reinterpret_cast<const f4*>(p.mask + row_off + col);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (!(mk[e] > 0.0f)) v[e] = 0.0f;
+      }
+      *reinterpret_cast<f4*>(C + row_off + col) = v;
+    }
+  }
+}
+
+template <bool A_KC, bool B_KC>
+__device__ void F32Dma::run(const F32Args& p, int bid, int split, float* smem) {
+  using OpA = Op<A_KC>;
+  using OpB = Op<B_KC>;
+  auto sA = [&](int buf) { return smem + buf * STAGE; };
+  auto sB = [&](int buf) { return smem + buf * STAGE + ELEMS; };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, r = lane & 15;
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * p.tiles_n;
+  const int grp = bid / per_group;
+  const int first_m = grp * GROUP;
+  const int gsize = min(p.tiles_m - first_m, GROUP);
+  const int in_grp = bid - grp * per_group;
+  const int tile_m = first_m + in_grp % gsize;
+  const int tile_n = in_grp / gsize;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+
+  const int kb = split * p.k_per_split;
+  const int nk = (min(p.K, kb + p.k_per_split) - kb) / BK;  // whole stages (checked by the host)
+
+  OpA oa;
+  OpB ob;
+  oa.init(A_KC ? p.A + (long long)m0 * p.lda + kb : p.A + (long long)kb * p.lda + m0, p.lda, wave, lane);
+  ob.init(B_KC ? p.B + (long long)n0 * p.ldb + kb : p.B + (long long)kb * p.ldb + n0, p.ldb, wave, lane);
+  const int a_step = 4 * (A_KC ? BK : BK * p.lda);  // bytes per stage
+  const int b_step = 4 * (B_KC ? BK : BK * p.ldb);
+  auto issue = [&](int stage, int buf) {
+    oa.issue(stage * a_step, sA(buf), wave);
+    ob.issue(stage * b_step, sB(buf), wave);
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int t = 0; t < TM; ++t)
+#pragma unroll
+    for (int u = 0; u < TN; ++u) acc[t][u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto read_frags = [&](int buf, int h, f4 (&fa)[TM], f4 (&fb)[TN]) {
+#pragma unroll
+    for (int u = 0; u < TN; ++u) fb[u] = OpB::frag(sB(buf), h, wn + 16 * u, g, r);
+#pragma unroll
+    for (int t = 0; t < TM; ++t) fa[t] = OpA::frag(sA(buf), h, wm + 16 * t, g, r);
+  };
+  auto mfmas = [&](const f4 (&fa)[TM], const f4 (&fb)[TN]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+#pragma unroll
+        for (int u = 0; u < TN; ++u)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(fb[u][s], fa[t][s], acc[t][u], 0, 0, 0);
+  };
+
+  // Bias gradient (TN with a colsum target, first M tile): thread t sums
+  // column t % 64 over the k rows 8 (t / 64) .. +7 of every stage; the four
+  // partial rows are added in order at the end.
+  const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0;  // uniform over the block
+  float cs = 0.0f;
+  auto colsum = [&](int buf) {
+    if constexpr (!B_KC) {
+      if (do_cs) {
+        const int col = tid & 63, k0 = 8 * (tid >> 6);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) cs += OpB::at(sB(buf), k0 + k, col);
+      }
+    }
+  };
+
+  if (nk > 0) {
+    f4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    // Every B step waits for everything and issues one stage (past the last
+    // stage it re-fetches stage nk-1 into a buffer nothing reads), so the
+    // bookkeeping is the same in every stage.
+    issue(0, 0);
+    issue(min(1, nk - 1), 1);
+    rt_dev::wait_vm<PER_STAGE>();
+    rt_dev::barrier_lds();
+    read_frags(0, 0, fa0, fb0);
+    auto stage = [&](int k, auto bc) {
+      constexpr int BUF = decltype(bc)::value;  // k % 2
+      read_frags(BUF, 1, fa1, fb1);
+      mfmas(fa0, fb0);
+      colsum(BUF);
+      rt_dev::wait_vm<0>();
+      rt_dev::barrier_lds();  // stage k+1 everywhere; stage k no longer read
+      issue(min(k + 2, nk - 1), BUF);
+      read_frags(BUF ^ 1, 0, fa0, fb0);  // (k+1, half 0); discarded after the last stage
+      mfmas(fa1, fb1);
+    };
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    for (int k = 0; k < nk; k += 2) {
+      stage(k, B0{});
+      if (k + 1 < nk) stage(k + 1, B1{});
+    }
+  }
+
+  if (do_cs) {
+    __syncthreads();  // main-loop LDS reads are finished
+    float* red = smem;  // [4][64]
+    red[tid] = cs;
+    __syncthreads();
+    if (tid < 64) {
+      const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
+      p.colsum[(long long)split * p.N + n0 + tid] = v;
+    }
+  }
+
+  if (p.splits > 1) return f32_store_direct<RT_EPI_NONE>(p, acc, m0, n0, wm, wn, g, r, split);
+  switch (p.epi) {
+    case RT_EPI_BIAS: return f32_store_direct<RT_EPI_BIAS>(p, acc, m0, n0, wm, wn, g, r, split);
+    case RT_EPI_BIAS_RELU: return f32_store_direct<RT_EPI_BIAS_RELU>(p, acc, m0, n0, wm, wn, g, r, split);
+    case RT_EPI_RELU_MASK: return f32_store_direct<RT_EPI_RELU_MASK>(p, acc, m0, n0, wm, wn, g, r, split);
+    default: return f32_store_direct<RT_EPI_NONE>(p, acc, m0, n0, wm, wn, g, r, split);
+  }
+}
+
+// Adapter so the single and pair kernels can run an F32Dma layout like an
+// F32Tile.
+template <bool A_KC, bool B_KC>
+struct F32DmaTile {
+  static constexpr int THREADS = F32Dma::THREADS;
+  static constexpr int SMEM = F32Dma::SMEM;
+  __device__ static void run(const F32Args& p, int bid, int split, float* smem) {
+    F32Dma::run<A_KC, B_KC>(p, bid, split, smem);
+  }
+};
+
 template <class T>
 __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(F32Args p) {
   __shared__ __attribute__((aligned(16))) float smem[T::SMEM];
@@ -448,12 +687,39 @@ TileCfg pick_tile(const F32Args& a) {
   return kT64;
 }
 
+// Whole 64x64 tiles, every K slice (the last included) a multiple of 32,
+// 16-byte aligned rows and pointers for the DMA and the float4 epilogue, and
+// operands addressable with 32-bit byte offsets.
+template <bool A_KC, bool B_KC>
+bool dma_ok(const F32Args& a) {
+  const int last = a.K - (a.splits - 1) * a.k_per_split;
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  const long long lim = 1LL << 31;
+  const bool epi_ok = (a.epi != RT_EPI_BIAS && a.epi != RT_EPI_BIAS_RELU) || al(a.bias);
+  const bool mask_ok = a.epi != RT_EPI_RELU_MASK || al(a.mask);
+  return a.M % 64 == 0 && a.N % 64 == 0 && a.k_per_split % 32 == 0 && last > 0 && last % 32 == 0 && a.vec_a &&
+         a.vec_b && a.vec_c && epi_ok && mask_ok && (long long)(A_KC ? a.M : a.K) * a.lda * 4 < lim &&
+         (long long)(B_KC ? a.N : a.K) * a.ldb * 4 < lim;
+}
+
+template <bool A_KC, bool B_KC>
+hipError_t launch_dma(hipStream_t s, F32Args a) {
+  using T = F32DmaTile<A_KC, B_KC>;
+  a.tiles_m = a.M / 64;
+  a.tiles_n = a.N / 64;
+  dim3 grid(a.tiles_m * a.tiles_n, 1, a.splits);
+  hipLaunchKernelGGL((gemm_f32_kernel<T>), grid, dim3(T::THREADS), 0, s, a);
+  return hipGetLastError();
+}
+
 template <bool A_KC, bool B_KC>
 hipError_t dispatch_tile(hipStream_t s, F32Args a) {
   switch (pick_tile(a)) {
     case kT128: return launch_f32<128, 128, A_KC, B_KC>(s, a);
     case kT64x32: return launch_f32<64, 32, A_KC, B_KC>(s, a);
-    default: return launch_f32<64, 64, A_KC, B_KC>(s, a);
+    default:
+      if (dma_ok<A_KC, B_KC>(a)) return launch_dma<A_KC, B_KC>(s, a);
+      return launch_f32<64, 64, A_KC, B_KC>(s, a);
   }
 }
 
@@ -488,10 +754,8 @@ F32Args make_args(const rt::GemmDesc& d) {
 // The backward pair of a hidden layer: dW = Aᵀ·δ (TN, 64x64 or, for a
 // narrow layer, 64x32 tiles; any number of K slices) and
 // dX = (δ·Wᵀ) ⊙ mask (NT, 64x64 tiles, whole K).
-template <int BN0>
+template <class T0, class T1, int BN0>
 hipError_t launch_pair_tn_nt(hipStream_t s, F32Args a0, F32Args a1) {
-  using T0 = F32Tile<64, BN0, false, false>;
-  using T1 = F32Tile<64, 64, true, true>;
   a0.tiles_m = (a0.M + 63) / 64;
   a0.tiles_n = (a0.N + BN0 - 1) / BN0;
   a1.tiles_m = (a1.M + 63) / 64;
@@ -530,8 +794,11 @@ bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1) {
 hipError_t gemm_pair_launch(hipStream_t s, const GemmDesc& d0, const GemmDesc& d1) {
   if (!gemm_pair_supported(d0, d1)) return hipErrorInvalidValue;
   const F32Args a0 = make_args(d0), a1 = make_args(d1);
-  if (pick_tile(a0) == kT64x32) return launch_pair_tn_nt<32>(s, a0, a1);
-  return launch_pair_tn_nt<64>(s, a0, a1);
+  if (pick_tile(a0) == kT64x32)
+    return launch_pair_tn_nt<F32Tile<64, 32, false, false>, F32Tile<64, 64, true, true>, 32>(s, a0, a1);
+  if (dma_ok<false, false>(a0) && dma_ok<true, true>(a1))
+    return launch_pair_tn_nt<F32DmaTile<false, false>, F32DmaTile<true, true>, 64>(s, a0, a1);
+  return launch_pair_tn_nt<F32Tile<64, 64, false, false>, F32Tile<64, 64, true, true>, 64>(s, a0, a1);
 }
 
 hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M, int N,

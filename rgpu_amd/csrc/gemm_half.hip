@@ -33,9 +33,14 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "device_util.h"
 #include "rt_internal.h"
 
 namespace {
+
+using rt_dev::barrier_lds;
+using rt_dev::static_for;
+using rt_dev::wait_vm;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u4 __attribute__((ext_vector_type(4)));
@@ -93,16 +98,6 @@ __device__ inline u4 load8(const unsigned short* base, int ld, int row, int col,
 #pragma unroll
   for (int d = 0; d < 4; ++d) v[d] = (unsigned int)h[2 * d] | ((unsigned int)h[2 * d + 1] << 16);
   return v;
-}
-
-// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E).  Used
-// where the body indexes the accumulator array, which must stay in registers.
-template <int B, int E, class F>
-__device__ inline void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
 }
 
 __device__ inline u2 lds_tr(const unsigned short* p) {
@@ -416,7 +411,7 @@ struct DmaOperand {
     static_assert(KC ? (RSTEP % 16 == 0) : (RSTEP % 8 == 0), "swizzle period");
     // 0x00020000: raw (untyped) buffer, 32-bit data format.  The host only
     // takes this path when every operand byte lies below 2^31 of its base.
-    rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(tile), (short)0, 0x7fffffff, 0x00020000);
+    rsrc = rt_dev::raw_rsrc(tile);
     row_bytes = 2 * ld;
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
@@ -431,17 +426,10 @@ struct DmaOperand {
     }
   }
   // This wave's DMA of the stage `stage_bytes` past the tile origin into `lds`.
-  // The scalar offset is made opaque to the optimiser, which would otherwise
-  // fold each instruction's uniform part into a separate VGPR offset.
   __device__ inline void issue(int stage_bytes, unsigned short* lds, int wave) const {
 #pragma unroll
-    for (int i = 0; i < PER_WAVE; ++i) {
-      int so = __builtin_amdgcn_readfirstlane(stage_bytes + i * RSTEP * row_bytes);
-      asm volatile("" : "+s"(so));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc,
-                                               (__attribute__((address_space(3))) void*)(lds + 512 * (i * WAVES + wave)),
-                                               16, voff[PAR ? (i & 1) : 0], so, 0, 0);
-    }
+    for (int i = 0; i < PER_WAVE; ++i)
+      rt_dev::dma16(rsrc, lds + 512 * (i * WAVES + wave), voff[PAR ? (i & 1) : 0], stage_bytes + i * RSTEP * row_bytes);
   }
   // Same fragment contract as Operand::frag.
   __device__ inline u4 frag(const unsigned short* lds, int kk, int rbase, int g, int r) const {
@@ -460,22 +448,6 @@ struct DmaOperand {
     return *reinterpret_cast<const u4*>(&lds[k * ROWS + 16 * ((c8 >> 1) ^ hm(k)) + 8 * (c8 & 1)]);
   }
 };
-
-// Workgroup barrier for the DMA pipeline: this wave's LDS reads are complete
-// (lgkmcnt 0), then s_barrier.  Unlike __syncthreads it does not wait for
-// outstanding global loads (the later stages in flight); the asm's memory
-// clobber keeps the compiler from moving LDS accesses across it.
-__device__ inline void barrier_lds() {
-  __builtin_amdgcn_s_waitcnt((0xF) | (0x3 << 14) | (0x7 << 4));  // lgkmcnt(0) only
-  asm volatile("s_barrier" ::: "memory");
-}
-
-// s_waitcnt vmcnt(N), leaving the LDS and export counters alone.
-template <int N>
-__device__ inline void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
 
 // Full-tile epilogue straight from the accumulators.  The DMA kernel issues
 // its MFMAs with the operands swapped (D = op(B)·op(A)), so lane (g, r) holds

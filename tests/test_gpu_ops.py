@@ -106,8 +106,10 @@ def test_gemm_large_tile_path(gpu):
         assert O.erro_rel(want, gpu.download(c)) < 1e-5, layout
 
 
-def test_gemm_epilogues(gpu):
-    m, n, k = 130, 200, 77
+# (130, 200, 77) takes the register-staged kernel; (128, 192, 96) is made of
+# whole 64x64 tiles and takes the direct-to-LDS one.
+@pytest.mark.parametrize("m,n,k", [(130, 200, 77), (128, 192, 96)])
+def test_gemm_epilogues(gpu, m, n, k):
     rng = np.random.default_rng(2)
     a = rng.normal(size=(m, k)).astype(np.float32)
     w = rng.normal(size=(k, n)).astype(np.float32)
@@ -131,7 +133,7 @@ def test_gemm_epilogues(gpu):
     assert np.all(got[act <= 0] == 0)
 
 
-@pytest.mark.parametrize("k,m,n", [(2048, 1024, 10), (64, 130, 96), (513, 64, 1024)])
+@pytest.mark.parametrize("k,m,n", [(2048, 1024, 10), (64, 130, 96), (513, 64, 1024), (256, 128, 192)])
 def test_tn_gemm_fused_colsum(gpu, k, m, n):
     rng = np.random.default_rng(3)
     x = rng.normal(size=(k, m)).astype(np.float32)
