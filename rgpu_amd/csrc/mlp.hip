@@ -76,6 +76,7 @@ struct rt_mlp {
   int t = 0;
   int dispatches = 0;
   bool mixed = false;
+  bool head_fused = false;  // output layer GEMM + softmax-xent in one launch
   const rt_buf* last_x = nullptr;
 };
 
@@ -148,7 +149,12 @@ static int plan_gemm(rt_mlp* p, const char* lbl, const char* lbl_red, int layout
   return finish_split(p, d, lbl_red, C, out_dtype, epi, bias, mask, mask_dtype, colsum);
 }
 
-static int run_forward(rt_mlp* p, const rt_buf* x) {
+// Forward pass; with labels, also the loss and δ of the output layer (scaled
+// by `scale`).  A narrow f32 output layer runs as one fused GEMM + softmax
+// cross-entropy launch; otherwise its GEMM (split-K when narrow) is followed
+// by the softmax cross-entropy launch.
+static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float scale) {
+  rt_ctx* c = p->ctx;
   const int nl = p->n_layers;
   const int B = (int)p->batch;
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
@@ -156,13 +162,28 @@ static int run_forward(rt_mlp* p, const rt_buf* x) {
     Layer& Ly = p->L[l];
     const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
     const bool last = l == nl - 1;
-    const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
     const float* bias = p->theta + Ly.b_off;
+    if (last && p->head_fused) {
+      Launch Lz(c, "head_xent");
+      hipError_t e = head_xent_launch(c->stream, (const float*)in, (int)Ly.din, p->theta + Ly.w_off, bias,
+                                      labels ? (const uint32_t*)labels->ptr : nullptr, (float*)Ly.act, Ly.delta,
+                                      p->loss_rows, B, (int)Ly.dout, scale / (float)B, c->d_flags);
+      if (e != hipSuccess) return hip_fail(c, e, "head_xent");
+      return RT_OK;
+    }
+    const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
     const int out_dtype = (p->mixed && !last) ? RT_BF16 : RT_F32;
     int rc = plan_gemm(p, Ly.lbl_fwd.c_str(), Ly.lbl_fwd_red.c_str(), RT_NN, in_dtype, in, W, Ly.act, out_dtype, B,
                        (int)Ly.dout, (int)Ly.din, (int)Ly.din, (int)Ly.dout, last ? RT_EPI_BIAS : RT_EPI_BIAS_RELU,
                        bias, nullptr, RT_F32, nullptr, Ly.splits_fwd);
     if (rc) return rc;
+  }
+  if (labels != nullptr) {
+    Layer& top = p->L[nl - 1];
+    Launch Lz(c, "softmax_xent");
+    hipError_t e = xent_launch(c->stream, (const float*)top.act, (const uint32_t*)labels->ptr, top.delta, top.delta_h,
+                               p->loss_rows, B, (int)top.dout, scale / (float)B, c->d_flags);
+    if (e != hipSuccess) return hip_fail(c, e, "softmax_xent");
   }
   return RT_OK;
 }
@@ -302,14 +323,18 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     Ly.pair_bwd = gemm_pair_supported(dw, dx);
   }
 
+  const Layer& top = p->L[n_layers - 1];
+  p->head_fused = !p->mixed && head_xent_supported((int)top.din, (int)top.dout);
+
   // Launch count of one step.
   int n = 0;
   for (int l = 0; l < n_layers; ++l) {
-    n += p->L[l].splits_fwd > 1 ? 2 : 1;
+    const bool fused = l == n_layers - 1 && p->head_fused;
+    n += fused ? 1 : (p->L[l].splits_fwd > 1 ? 2 : 1);
     n += p->L[l].splits_dw > 1 ? 2 : 1;
     if (l > 0 && !p->L[l].pair_bwd) n += 1;
   }
-  n += 1;  // softmax-xent
+  if (!p->head_fused) n += 1;  // softmax-xent
   n += 1;  // optimizer
   if (p->mixed) n += 2;  // step prologue + non-finite check
   p->dispatches = n;
@@ -353,15 +378,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     hipError_t e = step_begin_launch(c->stream, p->state);
     if (e != hipSuccess) return hip_fail(c, e, "step prologue");
   }
-  if ((rc = run_forward(p, x))) return rc;
-
-  Layer& top = p->L[nl - 1];
-  {
-    Launch Lz(c, "softmax_xent");
-    hipError_t e = xent_launch(c->stream, (const float*)top.act, (const uint32_t*)labels->ptr, top.delta, top.delta_h,
-                               p->loss_rows, B, (int)top.dout, scale / (float)B, c->d_flags);
-    if (e != hipSuccess) return hip_fail(c, e, "softmax_xent");
-  }
+  if ((rc = run_forward(p, x, labels, scale))) return rc;
 
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
   for (int l = nl - 1; l >= 0; --l) {
@@ -448,7 +465,7 @@ int rt_mlp_forward(rt_mlp* p, const rt_buf* x) {
   if (p == nullptr) return RT_ERR_INVALID;
   int rc = check_inputs(p, x);
   if (rc) return rc;
-  return run_forward(p, x);
+  return run_forward(p, x, nullptr, 1.0f);
 }
 
 int rt_mlp_logits(rt_mlp* p, float* host, size_t n) {

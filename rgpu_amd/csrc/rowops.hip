@@ -67,6 +67,93 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
   }
 }
 
+// Narrow output layer fused with the loss: z = A·W + b for C <= 16 classes
+// (rtensor runs the head GEMM with split-K and then XENT, mod.rs:1360-1367 and
+// 1399-1410), then the softmax cross-entropy of xent_kernel, in one launch.
+// Block = 16 rows and 8 waves; wave w sums k in [w K/8, (w+1) K/8) with
+// v_mfma_f32_16x16x4_f32, both operands straight from global memory (A as
+// float4 row segments, W as scalars, 8 chunks of 16 k in flight per batch).
+// Lane (g, r) feeds A(row r, k) and W(k, class r) with k = chunk + 4g + s at
+// MFMA step s, and ends with z(rows 4g..4g+3, class r).  The eight partial
+// tiles are added in LDS in wave order; then the 16 lanes of each row run
+// the softmax with width-16 shuffles.  With labels == null only the logits
+// are written.  The K sum order differs from the CPU path's; the rest
+// follows xent_kernel.
+typedef float f4v __attribute__((ext_vector_type(4)));
+constexpr int HEAD_C = 16, HEAD_ROWS = 16;
+
+__global__ __launch_bounds__(512) void head_xent_kernel(const float* __restrict__ A, int K,
+                                                        const float* __restrict__ W, const float* __restrict__ bias,
+                                                        const uint32_t* __restrict__ labels,
+                                                        float* __restrict__ logits, float* __restrict__ delta,
+                                                        float* __restrict__ loss_rows, int rows, int cols,
+                                                        float scale, int* err_flag) {
+  constexpr int HW = 8;  // waves
+  __shared__ float red[HW][HEAD_ROWS][HEAD_C + 1];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
+  const int r0 = blockIdx.x * HEAD_ROWS;
+  const int kq = K / HW;       // k per wave (K is a multiple of 128)
+  const int nch = kq / 16;     // chunks of 16 k per wave
+  const int kw = wave * kq;
+  const float* arow = A + (long long)min(r0 + r, rows - 1) * K + kw + 4 * g;  // rows past the end read the last row
+  f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+    f4v av[8];
+    float wv[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (c0 + i < nch) {
+        av[i] = *reinterpret_cast<const f4v*>(arow + 16 * (c0 + i));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int k = kw + 16 * (c0 + i) + 4 * g + s;
+          wv[i][s] = r < cols ? W[(long long)k * cols + r] : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (c0 + i < nch) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i][s], wv[i][s], acc, 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[wave][4 * g + q][r] = acc[q];
+  __syncthreads();
+
+  if (threadIdx.x >= HEAD_ROWS * HEAD_C) return;  // no barrier after this point
+  const int rr = threadIdx.x >> 4, cc = threadIdx.x & 15;  // one row per 16 lanes
+  const int row = r0 + rr;
+  float zs = red[0][rr][cc];
+#pragma unroll
+  for (int w = 1; w < HW; ++w) zs += red[w][rr][cc];
+  const float z = cc < cols ? zs + bias[cc] : -INFINITY;
+  if (row >= rows) return;
+  if (cc < cols) logits[(long long)row * cols + cc] = z;
+  if (labels == nullptr) return;
+  float mx = z;
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 16));
+  const float e = cc < cols ? expf(z - mx) : 0.0f;
+  float sum = e;
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
+  const uint32_t y = labels[row];
+  const bool bad = y >= (uint32_t)cols;
+  if (bad && cc == 0) {
+    *err_flag = 1;
+    loss_rows[row] = __uint_as_float(0x7fc00000u);
+  }
+  if (cc < cols) {
+    const float pj = e / sum;
+    const float yj = (!bad && (uint32_t)cc == y) ? 1.0f : 0.0f;
+    delta[(long long)row * cols + cc] = (pj - yj) * scale;
+    if (!bad && (uint32_t)cc == y) loss_rows[row] = -logf(fmaxf(pj, 1e-12f));
+  }
+}
+
 // Stage 1: block (cx, cy) sums rows [cy*chunk, (cy+1)*chunk) of 256 columns
 // starting at cx*256, one column per thread, rows in increasing order.
 template <typename T>
@@ -139,6 +226,19 @@ int grid_for(long long n) {
 }  // namespace
 
 namespace rt {
+
+bool head_xent_supported(int K, int cols) { return cols >= 1 && cols <= HEAD_C && K >= 128 && K % 128 == 0; }
+
+hipError_t head_xent_launch(hipStream_t s, const float* A, int K, const float* W, const float* bias,
+                            const uint32_t* labels, float* logits, float* delta, float* loss_rows, int rows, int cols,
+                            float scale, int* err_flag) {
+  if (!head_xent_supported(K, cols) || rows < 1 || (reinterpret_cast<uintptr_t>(A) & 15) != 0)
+    return hipErrorInvalidValue;
+  const unsigned blocks = (unsigned)((rows + HEAD_ROWS - 1) / HEAD_ROWS);
+  hipLaunchKernelGGL(head_xent_kernel, dim3(blocks), dim3(512), 0, s, A, K, W, bias, labels, logits, delta,
+                     loss_rows, rows, cols, scale, err_flag);
+  return hipGetLastError();
+}
 
 hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* labels, float* delta, void* delta_half,
                        float* loss_rows, int rows, int cols, float scale, int* err_flag) {

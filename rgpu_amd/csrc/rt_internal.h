@@ -112,6 +112,13 @@ hipError_t relu_launch(hipStream_t s, const float* x, float* y, size_t n);
 hipError_t relu_bwd_launch(hipStream_t s, const void* a, int a_dtype, float* delta, size_t n);
 hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* labels, float* delta, void* delta_half,
                        float* loss_rows, int rows, int cols, float scale, int* err_flag);
+// Output layer z = A·W + b (f32, cols <= 16 classes, K a multiple of 128, A
+// 16-byte aligned) fused with
+// the softmax cross-entropy of xent_launch; labels == nullptr writes only z.
+bool head_xent_supported(int K, int cols);
+hipError_t head_xent_launch(hipStream_t s, const float* A, int K, const float* W, const float* bias,
+                            const uint32_t* labels, float* logits, float* delta, float* loss_rows, int rows, int cols,
+                            float scale, int* err_flag);
 hipError_t convert_launch(hipStream_t s, const void* src, int src_dtype, void* dst, int dst_dtype, size_t n);
 hipError_t fill_i32_launch(hipStream_t s, int* p, int v, size_t n);
 
