@@ -47,6 +47,9 @@ struct Layer {
   int splits_dw = 1;
   int splits_fwd = 1;
   bool pair_bwd = false;  // dW and dX of this layer in one launch
+  // dW / db split-K planes of this layer summed by the optimizer (f32 plans):
+  // [splits_dw][din*dout] then [splits_dw][dout], owned by this layer.
+  float* dw_parts = nullptr;
   std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx, lbl_bwd;
 };
 
@@ -91,7 +94,7 @@ static bool valid_cfg(const rt_mlp_config* c) {
 // planes into the plan's partials buffer, summed by finish_split.
 static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, const void* B, void* C, int out_dtype,
                           int M, int N, int K, int lda, int ldb, int epi, const float* bias, const void* mask,
-                          int mask_dtype, float* colsum, int splits) {
+                          int mask_dtype, float* colsum, int splits, float* parts = nullptr) {
   GemmDesc d;
   d.layout = layout;
   d.in_dtype = in_dtype;
@@ -113,11 +116,12 @@ static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, co
     d.colsum = colsum;
     return d;
   }
-  d.C = p->partials;
+  if (parts == nullptr) parts = p->partials;
+  d.C = parts;
   d.out_dtype = RT_F32;
   d.splits = splits;
   d.split_stride = (long long)M * N;
-  d.colsum_partials = colsum ? p->partials + (size_t)splits * M * N : nullptr;
+  d.colsum_partials = colsum ? parts + (size_t)splits * M * N : nullptr;
   // Where the reduction puts the result and what it applies.
   d.epi = RT_EPI_NONE;
   return d;
@@ -188,6 +192,45 @@ static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float s
   return RT_OK;
 }
 
+// The optimizer's tensor list over the flat vectors: plain runs of segments
+// as one tensor each, and the W / b segments of layers whose dW planes are
+// still split as tensors that sum their planes first.
+static std::vector<OptTensor> opt_tensors(const rt_mlp* p) {
+  std::vector<OptTensor> ts;
+  auto seg = [&](size_t off, size_t n) {
+    OptTensor T{p->theta + off, p->grad + off, p->m + off, p->v + off,
+                p->theta_h ? (void*)((unsigned short*)p->theta_h + off) : nullptr, n};
+    return T;
+  };
+  size_t run0 = 0;
+  for (int l = 0; l < p->n_layers; ++l) {
+    const Layer& Ly = p->L[l];
+    if (Ly.dw_parts == nullptr) continue;
+    if (Ly.w_off > run0) ts.push_back(seg(run0, Ly.w_off - run0));
+    const size_t nw = Ly.din * Ly.dout;
+    OptTensor Tw = seg(Ly.w_off, nw);
+    Tw.parts = Ly.dw_parts;
+    Tw.n_parts = Ly.splits_dw;
+    Tw.part_stride = (long long)nw;
+    Tw.grad_store = p->grad + Ly.w_off;
+    ts.push_back(Tw);
+    OptTensor Tb = seg(Ly.b_off, Ly.dout);
+    Tb.parts = Ly.dw_parts + (size_t)Ly.splits_dw * nw;
+    Tb.n_parts = Ly.splits_dw;
+    Tb.part_stride = (long long)Ly.dout;
+    Tb.grad_store = p->grad + Ly.b_off;
+    ts.push_back(Tb);
+    run0 = Ly.b_off + Ly.dout;  // the b segment's padding stays untouched (zero)
+  }
+  if (run0 < p->n_params) ts.push_back(seg(run0, p->n_params - run0));
+  return ts;
+}
+
+static int opt_launches(const rt_mlp* p) {
+  const int n = (int)opt_tensors(p).size();
+  return (n + kMaxOptTensors - 1) / kMaxOptTensors;
+}
+
 namespace rt {
 void mlp_release(rt_mlp* p) {
   hipStreamSynchronize(p->ctx->stream);
@@ -243,10 +286,18 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   }
   p->n_params = off;
 
+  // Split-K planes: f32 plans keep each layer's dW planes until the optimizer
+  // sums them; everything else shares one buffer consumed right away.
   size_t part = 0;
-  for (auto& Ly : p->L) {
+  std::vector<size_t> dw_part_elems(n_layers, 0);
+  for (int l = 0; l < n_layers; ++l) {
+    const Layer& Ly = p->L[l];
     if (Ly.splits_fwd > 1) part = std::max(part, (size_t)Ly.splits_fwd * batch * Ly.dout);
-    if (Ly.splits_dw > 1) part = std::max(part, (size_t)Ly.splits_dw * (Ly.din * Ly.dout + Ly.dout));
+    if (Ly.splits_dw > 1) {
+      const size_t e = (size_t)Ly.splits_dw * (Ly.din * Ly.dout + Ly.dout);
+      if (p->mixed) part = std::max(part, e);
+      else dw_part_elems[l] = e;
+    }
   }
   p->partial_elems = part;
 
@@ -270,6 +321,9 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     o_delta_h[l] = p->mixed ? reserve(elems * 2) : 0;
   }
   size_t o_part = reserve(part * 4);
+  std::vector<size_t> o_dw_part(n_layers, 0);
+  for (int l = 0; l < n_layers; ++l)
+    if (dw_part_elems[l]) o_dw_part[l] = reserve(dw_part_elems[l] * 4);
   size_t o_loss = reserve(batch * 4);
   size_t o_state = reserve(16 * 4);
 
@@ -290,6 +344,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     p->L[l].delta_h = p->mixed ? (void*)(p->arena + o_delta_h[l]) : nullptr;
   }
   p->partials = part ? (float*)(p->arena + o_part) : nullptr;
+  for (int l = 0; l < n_layers; ++l) p->L[l].dw_parts = dw_part_elems[l] ? (float*)(p->arena + o_dw_part[l]) : nullptr;
   p->loss_rows = (float*)(p->arena + o_loss);
   p->state = (int*)(p->arena + o_state);
 
@@ -331,11 +386,11 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   for (int l = 0; l < n_layers; ++l) {
     const bool fused = l == n_layers - 1 && p->head_fused;
     n += fused ? 1 : (p->L[l].splits_fwd > 1 ? 2 : 1);
-    n += p->L[l].splits_dw > 1 ? 2 : 1;
+    n += (p->L[l].splits_dw > 1 && !p->L[l].dw_parts) ? 2 : 1;
     if (l > 0 && !p->L[l].pair_bwd) n += 1;
   }
   if (!p->head_fused) n += 1;  // softmax-xent
-  n += 1;  // optimizer
+  n += opt_launches(p);  // optimizer
   if (p->mixed) n += 2;  // step prologue + non-finite check
   p->dispatches = n;
   c->mlps.push_back(p);
@@ -388,7 +443,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     // dW_l = A_{l-1}ᵀ·δ_l  (TN; A stored [batch, din]), db_l = 1ᵀ·δ_l fused.
     const GemmDesc dw = plan_desc(p, RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32, (int)Ly.din, (int)Ly.dout,
                                   B, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32,
-                                  p->grad + Ly.b_off, Ly.splits_dw);
+                                  p->grad + Ly.b_off, Ly.splits_dw, Ly.dw_parts);
     if (l == 0) {
       {
         Launch Lz(c, Ly.lbl_dw.c_str());
@@ -419,9 +474,11 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
         if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dx.c_str());
       }
     }
-    rc = finish_split(p, dw, Ly.lbl_dw_red.c_str(), p->grad + Ly.w_off, RT_F32, RT_EPI_NONE, nullptr, nullptr, RT_F32,
-                      p->grad + Ly.b_off);
-    if (rc) return rc;
+    if (Ly.dw_parts == nullptr) {  // otherwise the optimizer sums the planes
+      rc = finish_split(p, dw, Ly.lbl_dw_red.c_str(), p->grad + Ly.w_off, RT_F32, RT_EPI_NONE, nullptr, nullptr,
+                        RT_F32, p->grad + Ly.b_off);
+      if (rc) return rc;
+    }
   }
 
   if (p->mixed) {
@@ -433,7 +490,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   }
 
   p->t += 1;
-  OptTensor T{p->theta, p->grad, p->m, p->v, p->theta_h, p->n_params};
+  std::vector<OptTensor> ts = opt_tensors(p);
   OptParams P;
   P.kind = p->cfg.optimizer == RT_OPT_ADAM ? 0 : 1;
   P.lr = p->cfg.lr;
@@ -454,10 +511,14 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     P.skip_flag = overflow;
     P.device_t = p->state;
   }
-  if (P.kind == 1 && P.momentum == 0.0f) T.m = nullptr;
-  Launch Lz(c, "optimizer");
-  hipError_t e = optimizer_launch(c->stream, &T, 1, P);
-  if (e != hipSuccess) return hip_fail(c, e, "optimizer");
+  if (P.kind == 1 && P.momentum == 0.0f)
+    for (auto& T : ts) T.m = nullptr;
+  for (size_t i0 = 0; i0 < ts.size(); i0 += kMaxOptTensors) {
+    const int nt = (int)std::min<size_t>(kMaxOptTensors, ts.size() - i0);
+    Launch Lz(c, "optimizer");
+    hipError_t e = optimizer_launch(c->stream, ts.data() + i0, nt, P);
+    if (e != hipSuccess) return hip_fail(c, e, "optimizer");
+  }
   return RT_OK;
 }
 

@@ -1,4 +1,6 @@
 // Fused optimizer: every parameter tensor of the model updated by ONE launch.
+// A tensor whose gradient is still split into K-slice partial planes is
+// reduced here (fixed slice order) instead of by a separate launch.
 //
 // rtensor's GPU plan issues one ADAM dispatch per tensor (mod.rs:1460-1467,
 // kernels.rs:205-224) and has no GPU SGD; here Adam and SGD share a single
@@ -49,41 +51,100 @@ __device__ inline float powi_dev(float a, int b) {
   return r;
 }
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+struct Coef {
+  float inv_c1, inv_c2;
+};
+
+// One element's update, the CPU expression order (optim.rs:88-95, 187-195).
+// m / v are read only where the method uses them.
+__device__ inline void update(const rt::OptParams& P, Coef c, float graw, float& th, float* m, float* v) {
+  const float g = graw * P.grad_scale;
+  if (P.kind == 0) {
+    const float mi = *m * P.beta1 + g * (1.0f - P.beta1);
+    const float vi = *v * P.beta2 + (g * g) * (1.0f - P.beta2);
+    *m = mi;
+    *v = vi;
+    const float m_hat = mi * c.inv_c1;
+    const float v_hat = vi * c.inv_c2;
+    th = th - (m_hat / (sqrtf(v_hat) + P.eps)) * P.lr;
+  } else if (P.momentum == 0.0f) {
+    th = th - g * P.lr;
+  } else {
+    const float vel = *m * P.momentum + g * P.lr;
+    *m = vel;
+    th = th - vel;
+  }
+}
+
+// Each thread owns 4 consecutive elements: one float4 of every stream when
+// the tensor allows it (T.vec), else four scalars.
 __global__ __launch_bounds__(kThreads) void optimizer_kernel(OptBatch b) {
   if (b.p.skip_flag != nullptr && *b.p.skip_flag != 0) return;
-  float inv_c1 = b.p.inv_c1, inv_c2 = b.p.inv_c2;
+  Coef c{b.p.inv_c1, b.p.inv_c2};
   if (b.p.device_t != nullptr) {
     const int t = *b.p.device_t + 1;
-    inv_c1 = 1.0f / (1.0f - powi_dev(b.p.beta1, t));
-    inv_c2 = 1.0f / (1.0f - powi_dev(b.p.beta2, t));
+    c.inv_c1 = 1.0f / (1.0f - powi_dev(b.p.beta1, t));
+    c.inv_c2 = 1.0f / (1.0f - powi_dev(b.p.beta2, t));
   }
   const int blk = blockIdx.x;
   int ti = 0;
   while (ti + 1 < b.nt && b.block_start[ti + 1] <= blk) ++ti;
   const rt::OptTensor& T = b.t[ti];
-  const long long base = (long long)(blk - b.block_start[ti]) * kPerBlock + threadIdx.x;
   const rt::OptParams& P = b.p;
+  const long long i0 = (long long)(blk - b.block_start[ti]) * kPerBlock + (long long)kPerThread * threadIdx.x;
+  if (i0 >= (long long)T.n) return;
+  const bool adam = P.kind == 0, has_m = T.m != nullptr;
+
+  if (T.vec && i0 + 4 <= (long long)T.n) {
+    f4 g;
+    if (T.parts != nullptr) {
+      g = *reinterpret_cast<const f4*>(T.parts + i0);
+#pragma unroll 4
+      for (int s = 1; s < T.n_parts; ++s) g = g + *reinterpret_cast<const f4*>(T.parts + (long long)s * T.part_stride + i0);
+      *reinterpret_cast<f4*>(T.grad_store + i0) = g;
+    } else {
+      g = *reinterpret_cast<const f4*>(T.grad + i0);
+    }
+    f4 th = *reinterpret_cast<const f4*>(T.theta + i0);
+    f4 m = has_m ? *reinterpret_cast<const f4*>(T.m + i0) : f4{0, 0, 0, 0};
+    f4 v = adam ? *reinterpret_cast<const f4*>(T.v + i0) : f4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float te = th[e], me = m[e], ve = v[e];
+      update(P, c, g[e], te, &me, &ve);
+      th[e] = te;
+      m[e] = me;
+      v[e] = ve;
+    }
+    *reinterpret_cast<f4*>(T.theta + i0) = th;
+    if (has_m) *reinterpret_cast<f4*>(T.m + i0) = m;
+    if (adam) *reinterpret_cast<f4*>(T.v + i0) = v;
+    if (T.half_copy != nullptr) {
+      unsigned short* h = static_cast<unsigned short*>(T.half_copy) + i0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16_rne(th[e]);
+    }
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < kPerThread; ++e) {
-    const long long i = base + (long long)e * kThreads;
+    const long long i = i0 + e;
     if (i >= (long long)T.n) break;
-    const float g = T.grad[i] * P.grad_scale;
-    float th = T.theta[i];
-    if (P.kind == 0) {
-      const float mi = T.m[i] * P.beta1 + g * (1.0f - P.beta1);
-      const float vi = T.v[i] * P.beta2 + (g * g) * (1.0f - P.beta2);
-      T.m[i] = mi;
-      T.v[i] = vi;
-      const float m_hat = mi * inv_c1;
-      const float v_hat = vi * inv_c2;
-      th = th - (m_hat / (sqrtf(v_hat) + P.eps)) * P.lr;
-    } else if (P.momentum == 0.0f) {
-      th = th - g * P.lr;
+    float graw;
+    if (T.parts != nullptr) {
+      graw = T.parts[i];
+      for (int s = 1; s < T.n_parts; ++s) graw = graw + T.parts[(long long)s * T.part_stride + i];
+      T.grad_store[i] = graw;
     } else {
-      const float vel = T.m[i] * P.momentum + g * P.lr;
-      T.m[i] = vel;
-      th = th - vel;
+      graw = T.grad[i];
     }
+    float th = T.theta[i];
+    float mi = has_m ? T.m[i] : 0.0f, vi = adam ? T.v[i] : 0.0f;
+    update(P, c, graw, th, &mi, &vi);
+    if (has_m) T.m[i] = mi;
+    if (adam) T.v[i] = vi;
     T.theta[i] = th;
     if (T.half_copy != nullptr) static_cast<unsigned short*>(T.half_copy)[i] = f32_to_bf16_rne(th);
   }
@@ -146,8 +207,15 @@ hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const Op
   b.nt = nt;
   b.p = p;
   long long blocks = 0;
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   for (int i = 0; i < nt; ++i) {
     b.t[i] = ts[i];
+    const OptTensor& T = ts[i];
+    // float4 streams: every base 16-byte aligned (the bf16 copy 8-byte) and
+    // the partial planes 4-float strided.
+    b.t[i].vec = al16(T.theta) && al16(T.grad) && (T.m == nullptr || al16(T.m)) && (T.v == nullptr || al16(T.v)) &&
+                 (T.half_copy == nullptr || (reinterpret_cast<uintptr_t>(T.half_copy) & 7) == 0) &&
+                 (T.parts == nullptr || (al16(T.parts) && al16(T.grad_store) && T.part_stride % 4 == 0));
     b.block_start[i] = (int)blocks;
     blocks += (long long)((ts[i].n + kPerBlock - 1) / kPerBlock);
   }

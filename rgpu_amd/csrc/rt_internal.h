@@ -130,6 +130,14 @@ struct OptTensor {
   float* v;           // Adam second moment
   void* half_copy;    // optional bf16 copy of theta written after the update
   size_t n;
+  // Deferred split-K reduction: when parts is set the gradient is the sum of
+  // the n_parts planes parts[s * part_stride + i] in slice order (exactly what
+  // splitk_reduce computes) and is also stored to grad_store[i].
+  const float* parts = nullptr;
+  int n_parts = 0;
+  long long part_stride = 0;
+  float* grad_store = nullptr;
+  bool vec = false;  // set by optimizer_launch: float4 streams are aligned
 };
 struct OptParams {
   int kind = 0;  // 0 Adam, 1 SGD

@@ -76,12 +76,13 @@ def test_training_follows_cpu_trajectory(gpu):  # gpu.rs:99-139
 def test_narrow_output_layer_uses_split_k_and_follows_cpu(gpu):  # gpu.rs:145-213
     x, lab = quadrant_data(512, 8)
     loss, mlp = _trajectory(gpu, x, lab, [8, 128, 4], 7, 60, 0.05)
-    # Launches: hidden forward 1 + output layer fused with the loss 1 + dW per
-    # layer (1, or 2 when split-K: the narrow output dW (128x4, K=512) is
-    # split; the output layer's dX shares the launch of its dW) + optimizer 1.
+    # Launches: hidden forward 1 + output layer fused with the loss 1 + one dW
+    # launch per layer (the narrow output dW (128x4, K=512) is split-K and the
+    # optimizer sums its planes; the output layer's dX shares the launch of
+    # its dW) + optimizer 1.
     s_dw = [G.Gpu.fatias_sugeridas(8, 128, 512), G.Gpu.fatias_sugeridas(128, 4, 512)]
     assert s_dw[1] > 1, "the narrow dW must be split"
-    want = 1 + 1 + sum(2 if s > 1 else 1 for s in s_dw) + 1
+    want = 1 + 1 + len(s_dw) + 1
     assert mlp.dispatches_por_passo() == want
     assert loss < 0.2
 
