@@ -181,6 +181,34 @@ int rt_mlp_dispatches(rt_mlp* mlp, int* out);
  * under loss scaling (blocking). */
 int rt_mlp_overflow(rt_mlp* mlp, int* out);
 
+/* ------------------------------------------------- checkpoint and resume */
+
+/* Param::set (tape.rs:119-121) for every parameter of the plan: n = 2 x layers
+ * host arrays in parameter order [W1, b1, ...] (W [in, out], b [1, out]).
+ * Refreshes the bf16 weight copy under mixed precision.  Blocking. */
+int rt_mlp_set_weights(rt_mlp* mlp, const float* const* host, int n);
+
+/* Optimizer state, which rtensor's GpuMlp keeps private (mod.rs:1291-1314,
+ * 1334): the first and second moments (Adam m, v; SGD keeps its velocity in
+ * m) per parameter, in the order of rt_mlp_weights, and t, the number of
+ * updates applied so far (under loss scaling, skipped steps do not count).
+ * A null m or v array list skips that part.  get blocks; set takes effect for
+ * the next step. */
+int rt_mlp_get_optimizer_state(rt_mlp* mlp, float* const* m, float* const* v, int n, int* t);
+int rt_mlp_set_optimizer_state(rt_mlp* mlp, const float* const* m, const float* const* v, int n, int t);
+
+/* ------------------------------------------------------------- inference */
+
+/* Tensor::argmax_rows (tensor.rs:476-493) on the device: out[r] is the first
+ * index of the maximum of row r of logits f32 [B, C].  As in the reference, a
+ * NaN in column 0 wins its row and later NaNs never do.  out: u32 [B]. */
+int rt_argmax_rows(rt_ctx* ctx, const rt_buf* logits, rt_buf* out);
+
+/* losses::accuracy (losses.rs:181-185): the fraction of rows whose argmax
+ * equals the label, hits / B in f32 (0 for B = 0).  labels: u32 [B].
+ * Blocking. */
+int rt_accuracy(rt_ctx* ctx, const rt_buf* logits, const rt_buf* labels, float* out);
+
 /* ------------------------------------------------------------- profiling */
 
 /* Gpu::perfilar (mod.rs:1245-1286): while enabled, every launch on ctx is

@@ -579,6 +579,70 @@ static int fetch(rt_mlp* p, const float* base, float* const* host, int n) {
   return RT_OK;
 }
 
+static int put(rt_mlp* p, float* base, const float* const* host, int n) {
+  rt_ctx* c = p->ctx;
+  if (host == nullptr || n != 2 * p->n_layers) return fail(c, RT_ERR_SHAPE, "need %d host arrays", 2 * p->n_layers);
+  for (int i = 0; i < n; ++i)
+    if (host[i] == nullptr) return fail(c, RT_ERR_INVALID, "null host array %d", i);
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < p->n_layers && e == hipSuccess; ++l) {
+    const Layer& Ly = p->L[l];
+    e = hipMemcpyAsync(base + Ly.w_off, host[2 * l], Ly.din * Ly.dout * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(base + Ly.b_off, host[2 * l + 1], Ly.dout * 4, hipMemcpyHostToDevice, c->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "upload parameters");
+  return RT_OK;
+}
+
+int rt_mlp_set_weights(rt_mlp* p, const float* const* host, int n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  int rc = put(p, p->theta, host, n);
+  if (rc || !p->mixed) return rc;
+  rt_ctx* c = p->ctx;
+  hipError_t e = convert_launch(c->stream, p->theta, RT_F32, p->theta_h, RT_BF16, p->n_params);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "bf16 weight copy");
+  return RT_OK;
+}
+
+int rt_mlp_get_optimizer_state(rt_mlp* p, float* const* m, float* const* v, int n, int* t) {
+  if (p == nullptr || t == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  int rc;
+  if (m != nullptr && (rc = fetch(p, p->m, m, n))) return rc;
+  if (v != nullptr && (rc = fetch(p, p->v, v, n))) return rc;
+  if (!p->mixed) {
+    *t = p->t;
+    return RT_OK;
+  }
+  // Device count of applied updates, plus the last step if it was issued and
+  // did not overflow (step_begin_launch folds that in at the next step).
+  int st[3] = {0, 0, 0};
+  hipError_t e = hipMemcpyAsync(st, p->state, sizeof st, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e != hipSuccess) return hip_fail(c, e, "optimizer state");
+  *t = st[0] + ((st[2] != 0 && st[1] == 0) ? 1 : 0);
+  return RT_OK;
+}
+
+int rt_mlp_set_optimizer_state(rt_mlp* p, const float* const* m, const float* const* v, int n, int t) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  if (t < 0) return fail(c, RT_ERR_INVALID, "t must be >= 0");
+  int rc;
+  if (m != nullptr && (rc = put(p, p->m, m, n))) return rc;
+  if (v != nullptr && (rc = put(p, p->v, v, n))) return rc;
+  p->t = t;
+  if (p->mixed) {
+    const int st[3] = {t, 0, 0};  // t applied updates, no overflow, no step pending
+    hipError_t e = hipMemcpyAsync(p->state, st, sizeof st, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return hip_fail(c, e, "optimizer state");
+  }
+  return RT_OK;
+}
+
 int rt_mlp_weights(rt_mlp* p, float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
   return fetch(p, p->theta, host, n);

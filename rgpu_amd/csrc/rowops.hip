@@ -154,6 +154,43 @@ __global__ __launch_bounds__(512) void head_xent_kernel(const float* __restrict_
   }
 }
 
+// Row argmax with Tensor::argmax_rows' semantics (tensor.rs:476-493): the
+// first index j with j == 0 or z_j > (best so far).  Hence a NaN in column 0
+// wins the row, later NaNs never win, and ties go to the first index.  As a
+// reduction: if z_0 is NaN the answer is 0, else the first index of the
+// largest non-NaN value (column 0 is non-NaN then, so one exists).  One wave
+// per row; lanes scan strided columns, then (value, index) pairs are combined
+// with "larger value, or equal value and smaller index".
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ z, uint32_t* __restrict__ out, int rows,
+                                                     int cols) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* zr = z + (long long)row * cols;
+  float bv = -INFINITY;
+  int bj = 0x7fffffff;
+  for (int j = lane; j < cols; j += 64) {
+    const float v = zr[j];
+    if (!(v != v) && (bj == 0x7fffffff || v > bv)) {  // strided scan: keep the first max of this lane
+      bv = v;
+      bj = j;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oj = __shfl_xor(bj, off, 64);
+    if (oj != 0x7fffffff && (bj == 0x7fffffff || ov > bv || (ov == bv && oj < bj))) {
+      bv = ov;
+      bj = oj;
+    }
+  }
+  if (lane == 0) {
+    const float z0 = zr[0];
+    out[row] = (z0 != z0 || bj == 0x7fffffff) ? 0u : (uint32_t)bj;
+  }
+}
+
 // Stage 1: block (cx, cy) sums rows [cy*chunk, (cy+1)*chunk) of 256 columns
 // starting at cx*256, one column per thread, rows in increasing order.
 template <typename T>
@@ -237,6 +274,12 @@ hipError_t head_xent_launch(hipStream_t s, const float* A, int K, const float* W
   const unsigned blocks = (unsigned)((rows + HEAD_ROWS - 1) / HEAD_ROWS);
   hipLaunchKernelGGL(head_xent_kernel, dim3(blocks), dim3(512), 0, s, A, K, W, bias, labels, logits, delta,
                      loss_rows, rows, cols, scale, err_flag);
+  return hipGetLastError();
+}
+
+hipError_t argmax_launch(hipStream_t s, const float* z, uint32_t* out, int rows, int cols) {
+  if (rows < 1 || cols < 1) return hipSuccess;
+  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, out, rows, cols);
   return hipGetLastError();
 }
 

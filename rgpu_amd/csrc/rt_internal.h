@@ -119,6 +119,9 @@ bool head_xent_supported(int K, int cols);
 hipError_t head_xent_launch(hipStream_t s, const float* A, int K, const float* W, const float* bias,
                             const uint32_t* labels, float* logits, float* delta, float* loss_rows, int rows, int cols,
                             float scale, int* err_flag);
+// out[r] = Tensor::argmax_rows of row r of z [rows, cols] (first max; a NaN in
+// column 0 wins the row, later NaNs never do).
+hipError_t argmax_launch(hipStream_t s, const float* z, uint32_t* out, int rows, int cols);
 hipError_t convert_launch(hipStream_t s, const void* src, int src_dtype, void* dst, int dst_dtype, size_t n);
 hipError_t fill_i32_launch(hipStream_t s, int* p, int v, size_t n);
 

@@ -561,6 +561,58 @@ int rt_softmax_xent(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, rt_bu
   return RT_OK;
 }
 
+int rt_argmax_rows(rt_ctx* c, const rt_buf* logits, rt_buf* out) {
+  CHECK_CTX(c);
+  if (!logits || !out) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (logits->rank != 2 || logits->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "logits must be f32 [B, C]");
+  const size_t B = logits->shape[0], Cc = logits->shape[1];
+  if (out->dtype != RT_U32 || out->n != B) return fail(c, RT_ERR_SHAPE, "out must be u32 [%zu]", B);
+  if (Cc == 0 && B > 0) return fail(c, RT_ERR_SHAPE, "zero classes");
+  if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "too large");
+  if (B == 0) return RT_OK;
+  Launch L(c, "argmax");
+  HIP_TRY(c,
+          argmax_launch(c->stream, static_cast<const float*>(logits->ptr), static_cast<uint32_t*>(out->ptr), (int)B,
+                        (int)Cc),
+          "argmax");
+  return RT_OK;
+}
+
+int rt_accuracy(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, float* out) {
+  CHECK_CTX(c);
+  if (!logits || !labels || !out) return fail(c, RT_ERR_INVALID, "null argument");
+  if (logits->rank != 2 || logits->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "logits must be f32 [B, C]");
+  const size_t B = logits->shape[0], Cc = logits->shape[1];
+  if (labels->dtype != RT_U32 || labels->n != B) return fail(c, RT_ERR_SHAPE, "labels must be u32 [%zu]", B);
+  if (B == 0) {
+    *out = 0.0f;
+    return RT_OK;
+  }
+  if (Cc == 0) return fail(c, RT_ERR_SHAPE, "zero classes");
+  if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "too large");
+  // Predictions in the context scratch (grow-only), then compared on the host.
+  if (c->scratch_elems < B) {
+    if (c->scratch) HIP_TRY(c, hipFree(c->scratch), "scratch free");
+    c->scratch = nullptr;
+    c->scratch_elems = 0;
+    HIP_TRY(c, hipMalloc(&c->scratch, B * sizeof(float)), "scratch");
+    c->scratch_elems = B;
+  }
+  uint32_t* pred = reinterpret_cast<uint32_t*>(c->scratch);
+  {
+    Launch L(c, "argmax");
+    HIP_TRY(c, argmax_launch(c->stream, static_cast<const float*>(logits->ptr), pred, (int)B, (int)Cc), "argmax");
+  }
+  std::vector<uint32_t> hp(B), hl(B);
+  HIP_TRY(c, hipMemcpyAsync(hp.data(), pred, B * 4, hipMemcpyDeviceToHost, c->stream), "download");
+  HIP_TRY(c, hipMemcpyAsync(hl.data(), labels->ptr, B * 4, hipMemcpyDeviceToHost, c->stream), "download");
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "sync");
+  size_t hits = 0;
+  for (size_t i = 0; i < B; ++i) hits += hp[i] == hl[i];
+  *out = (float)hits / (float)B;
+  return RT_OK;
+}
+
 int rt_adam(rt_ctx* c, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, float lr, float beta1, float beta2,
             float eps, int t) {
   CHECK_CTX(c);

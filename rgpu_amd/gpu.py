@@ -91,6 +91,13 @@ SIGNATURES = {
                                     C.c_int, C.POINTER(C.c_int)]),
     "rt_timer_begin": (C.c_int, [_VP]),
     "rt_timer_end": (C.c_int, [_VP, C.POINTER(C.c_float)]),
+    "rt_mlp_set_weights": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.c_int]),
+    "rt_mlp_get_optimizer_state": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.POINTER(C.c_float)),
+                                             C.c_int, C.POINTER(C.c_int)]),
+    "rt_mlp_set_optimizer_state": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.POINTER(C.c_float)),
+                                             C.c_int, C.c_int]),
+    "rt_argmax_rows": (C.c_int, [_VP, _VP, _VP]),
+    "rt_accuracy": (C.c_int, [_VP, _VP, _VP, C.POINTER(C.c_float)]),
 }
 
 
@@ -308,6 +315,16 @@ class Gpu:
     def sgd(self, theta, g, lr: float, momentum: float = 0.0, velocity: Optional[GpuTensor] = None):
         self._call("rt_sgd", self._h, theta.handle, velocity.handle if velocity else None, g.handle, lr, momentum)
 
+    def argmax_rows(self, logits, out):
+        """Tensor::argmax_rows (tensor.rs:476-493) into a u32 [B] device buffer."""
+        self._call("rt_argmax_rows", self._h, logits.handle, out.handle)
+
+    def accuracy(self, logits, labels) -> float:
+        """losses::accuracy (losses.rs:181-185) of device logits against u32 labels."""
+        v = C.c_float()
+        self._call("rt_accuracy", self._h, logits.handle, labels.handle, C.byref(v))
+        return v.value
+
     # --------------------------------------------------------------- profiling
     def profile(self, on: bool) -> None:
         self._call("rt_profile_enable", self._h, 1 if on else 0)
@@ -420,6 +437,64 @@ class GpuMlp:
 
     def weights(self) -> List[np.ndarray]:
         return self._fetch("rt_mlp_weights")
+
+    @staticmethod
+    def _ptrs(arrs):
+        return (C.POINTER(C.c_float) * len(arrs))(*[a.ctypes.data_as(C.POINTER(C.c_float)) for a in arrs])
+
+    def _checked(self, arrs) -> List[np.ndarray]:
+        shapes = self._shapes()
+        if len(arrs) != len(shapes):
+            raise ValueError(f"need {len(shapes)} arrays, got {len(arrs)}")
+        out = []
+        for a, shp in zip(arrs, shapes):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            if a.size != int(np.prod(shp)):
+                raise ValueError(f"array of {a.size} elements for a parameter of shape {shp}")
+            out.append(a)
+        return out
+
+    def set_weights(self, arrs) -> None:
+        """Param::set (tape.rs:119-121) for every parameter, in parameter order."""
+        arrs = self._checked(arrs)
+        self.gpu._call("rt_mlp_set_weights", self._h, self._ptrs(arrs), len(arrs))
+
+    def optimizer_state(self):
+        """(m, v, t): the optimizer's moments per parameter and the applied-update count."""
+        m = [np.empty(s, np.float32) for s in self._shapes()]
+        v = [np.empty(s, np.float32) for s in self._shapes()]
+        t = C.c_int()
+        self.gpu._call("rt_mlp_get_optimizer_state", self._h, self._ptrs(m), self._ptrs(v), len(m), C.byref(t))
+        return m, v, t.value
+
+    def set_optimizer_state(self, m, v, t: int) -> None:
+        m, v = self._checked(m), self._checked(v)
+        self.gpu._call("rt_mlp_set_optimizer_state", self._h, self._ptrs(m), self._ptrs(v), len(m), int(t))
+
+    def state_dict(self) -> dict:
+        """Everything a resumed run needs: weights, optimizer moments and t."""
+        m, v, t = self.optimizer_state()
+        return {"weights": self.weights(), "m": m, "v": v, "t": t}
+
+    def load_state_dict(self, state: dict) -> None:
+        self.set_weights(state["weights"])
+        self.set_optimizer_state(state["m"], state["v"], state["t"])
+
+    def save(self, path: str) -> None:
+        """Checkpoint to an .npz file (plain arrays, no pickled objects)."""
+        st = self.state_dict()
+        arrays = {"t": np.array([st["t"]], np.int64)}
+        for key in ("weights", "m", "v"):
+            for i, a in enumerate(st[key]):
+                arrays[f"{key}_{i}"] = a
+        np.savez(path, **arrays)
+
+    def load(self, path: str) -> None:
+        n = len(self._shapes())
+        with np.load(path, allow_pickle=False) as z:
+            st = {key: [z[f"{key}_{i}"] for i in range(n)] for key in ("weights", "m", "v")}
+            st["t"] = int(z["t"][0])
+        self.load_state_dict(st)
 
     def grads(self) -> List[np.ndarray]:
         return self._fetch("rt_mlp_grads")

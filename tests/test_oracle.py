@@ -103,6 +103,15 @@ def test_argmax_first_max_wins():
     assert O.accuracy(z, [1, 0, 2]) == pytest.approx(2 / 3)
 
 
+def test_argmax_nan_and_infinity_cases():
+    # tensor.rs:484-488 takes j == 0 or v > best: a NaN in column 0 keeps the
+    # row, a later NaN is never taken, -inf rows give 0, -0 and +0 tie.
+    nan, inf = np.nan, np.inf
+    z = np.array([[nan, 1, 2], [1, nan, 3], [1, nan, 0], [-inf, -inf, -inf], [-0.0, 0.0, -inf],
+                  [-inf, nan, -1], [inf, inf, 1]], np.float32)
+    assert O.argmax_rows(z).tolist() == [0, 2, 0, 0, 0, 2, 0]
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (17, 33, 65), (64, 64, 64), (65, 64, 63), (130, 96, 80),
                                    (199, 130, 71), (256, 512, 128)])
 def test_matmul_against_float64(m, n, k):
