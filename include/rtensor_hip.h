@@ -4,7 +4,7 @@
  * The backend replaces rtensor's wgpu module (crates/rtensor/src/gpu/mod.rs)
  * for the MLP training step.  Each entry point below names the rtensor::gpu
  * call it stands in for (file:line in the rtensor crate).  A Rust FFI crate
- * binds these symbols one-for-one; see INTEGRATION.md for the binding.
+ * binds these symbols one-for-one.
  *
  * Conventions
  *   - Every function returns an int status (rt_status); 0 is success.  The
@@ -17,6 +17,10 @@
  *     Gpu::record + Gpu::submit (mod.rs:609, 1231-1237); rt_download,
  *     rt_sync and the rt_mlp_* readers block, like Gpu::download
  *     (mod.rs:530-544).  An rt_ctx is not thread-safe, as Gpu is not Send.
+ *   - Freed buffers return to a per-context cache and are reused by later
+ *     allocations of the same size class; device memory is given back by
+ *     rt_close (or when an allocation would otherwise fail).  Reuse is safe
+ *     because all work of a context runs in order on its one stream.
  *   - Tensors are dense row-major.  Weights are [in, out], biases [1, out],
  *     parameters travel in the order [W1, b1, W2, b2, ...] (nn.rs:190-192).
  *     Labels are u32 (mod.rs:1672-1675).
@@ -196,6 +200,79 @@ int rt_mlp_set_weights(rt_mlp* mlp, const float* const* host, int n);
  * the next step. */
 int rt_mlp_get_optimizer_state(rt_mlp* mlp, float* const* m, float* const* v, int n, int* t);
 int rt_mlp_set_optimizer_state(rt_mlp* mlp, const float* const* m, const float* const* v, int n, int t);
+
+/* ------------------------------------------------------------- tensor ops
+ * Device versions of the Tensor operations rtensor's autodiff tape records
+ * (tensor.rs, ops.rs, losses.rs), so a Tape/Sequential model of any shape
+ * trains on the device; matmul and its VJPs are rt_gemm (RT_NN, RT_NT, RT_TN
+ * = tensor.rs:318 and ops.rs:125-129).  All f32, rank <= 4, enqueue only.
+ * Elementwise results round exactly like the reference except where a
+ * transcendental (exp, ln, tanh, sqrt is exact) differs in its last bits;
+ * rt_reduce_to is exact; rt_sum_all and rt_loss add in a fixed tree order
+ * instead of the reference's left-to-right loop. */
+
+typedef enum {
+  RT_U_SCALE = 0,      /* v * k                 ops.rs:132-135 */
+  RT_U_OFFSET = 1,     /* v + k                 ops.rs:139-142 */
+  RT_U_NEG = 2,        /* v * -1                ops.rs:145-147 */
+  RT_U_SQUARE = 3,     /* v * v                 ops.rs:150-154 */
+  RT_U_SQRT = 4,       /* sqrt(v)               ops.rs:158-162 */
+  RT_U_EXP = 5,        /* exp(v)                ops.rs:166-170 */
+  RT_U_LN = 6,         /* ln(max(v, 1e-12))     ops.rs:176-180 */
+  RT_U_RELU = 7,       /* max(v, 0)             ops.rs:190-194 */
+  RT_U_LEAKY_RELU = 8, /* v > 0 ? v : k v       ops.rs:197-203 */
+  RT_U_SIGMOID = 9,    /* 1 / (1 + exp(-v))     ops.rs:212-216 */
+  RT_U_TANH = 10       /* tanh(v)               ops.rs:223-227 */
+} rt_unary_op;
+
+typedef enum { RT_B_ADD = 0, RT_B_SUB = 1, RT_B_MUL = 2, RT_B_DIV = 3 } rt_binary_op;
+
+typedef enum {
+  RT_LOSS_MAE = 1,          /* losses.rs:46-53, on d = pred - target       */
+  RT_LOSS_SOFTMAX_XENT = 2, /* losses.rs:99-115, on p = softmax_rows(z)    */
+  RT_LOSS_BCE = 3           /* losses.rs:143-162, on probabilities         */
+} rt_loss_kind;             /* mse (losses.rs:31-34) is sub, square, mean   */
+
+/* Tensor::map (tensor.rs:160-181) with the forward closure of op:
+ * y = f(x), same element count. */
+int rt_map(rt_ctx* ctx, rt_unary_op op, float k, const rt_buf* x, rt_buf* y);
+/* The VJP closure of op (ops.rs:132-227): dx from the upstream g, the op's
+ * input x and its output y.  x is needed by SQUARE, LN, RELU, LEAKY_RELU;
+ * y by SQRT, EXP, SIGMOID, TANH; either may be NULL when unused. */
+int rt_map_vjp(rt_ctx* ctx, rt_unary_op op, float k, const rt_buf* g, const rt_buf* x, const rt_buf* y,
+               rt_buf* dx);
+/* Tensor::zip (tensor.rs:183-246) with numpy broadcasting
+ * (broadcast_shapes, tensor.rs:575-592): out must have the broadcast shape.
+ * out may alias a or b only when it has that operand's shape. */
+int rt_zip(rt_ctx* ctx, rt_binary_op op, const rt_buf* a, const rt_buf* b, rt_buf* out);
+/* Tensor::reduce_to (tensor.rs:399-438): out's shape is the target, right-
+ * aligned against g's, each axis equal to g's or 1.  Every output element
+ * sums its sources in increasing index order, as the reference does (exact),
+ * except a one-element target, which is rt_sum_all. */
+int rt_reduce_to(rt_ctx* ctx, const rt_buf* g, rt_buf* out);
+/* sum_all / mean_all (tensor.rs:279-286): out[0] = (sum of x) / div, out has
+ * one element.  div = 1 for sum, len(x) for mean. */
+int rt_sum_all(rt_ctx* ctx, const rt_buf* x, float div, rt_buf* out);
+/* The scalar-scaled VJPs (ops.rs:239-255, losses.rs:53, 114, 160):
+ * out[i] = x[i] * (s[0] / div), or s[0] / div everywhere (Tensor::full) when
+ * x is NULL.  s has one element; x, if given, has out's element count. */
+int rt_fill_scaled(rt_ctx* ctx, const rt_buf* s, float div, const rt_buf* x, rt_buf* out);
+/* Tensor::softmax_rows (tensor.rs:455-472) of z [R, C] into y [R, C]. */
+int rt_softmax_rows(rt_ctx* ctx, const rt_buf* z, rt_buf* y);
+/* softmax's VJP (ops.rs:291-309): dx = s ⊙ (g − rowsum(g ⊙ s)), s the
+ * forward output. */
+int rt_softmax_rows_vjp(rt_ctx* ctx, const rt_buf* s, const rt_buf* g, rt_buf* dx);
+/* Loss value and unscaled gradient direction (losses.rs): value[0] = total /
+ * batch (batch = rows of p for softmax-xent, len(p) otherwise); dir (NULL to
+ * skip) = sign(d), p − y, or (c − y)/(c(1 − c)) with c = clamp(p, 1e-7,
+ * 1 − 1e-7).  The loss node's VJP is rt_fill_scaled(g, batch, dir).  y is
+ * NULL for RT_LOSS_MAE (p is already pred − target). */
+int rt_loss(rt_ctx* ctx, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_buf* value, rt_buf* dir);
+
+/* Gpu::zeros without the zero fill (contents undefined), for op outputs
+ * that are written whole.  No counterpart in rtensor (wgpu buffers start
+ * zeroed). */
+int rt_empty(rt_ctx* ctx, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out);
 
 /* ------------------------------------------------------------- inference */
 

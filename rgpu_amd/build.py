@@ -29,6 +29,7 @@ SOURCES = {
     "gemm_half.hip": [],
     "rowops.hip": ["-ffp-contract=off"],
     "optim.hip": ["-ffp-contract=off"],
+    "tensor_ops.hip": ["-ffp-contract=off"],
 }
 
 COMMON = [

@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstdint>
 #include <string>
+#include <unordered_map>
+#include <unordered_set>
 #include <vector>
 
 #include "rtensor_hip.h"
@@ -17,6 +19,7 @@ struct rt_buf {
   int rank = 0;
   size_t n = 0;      // elements
   size_t bytes = 0;  // n * element size
+  size_t cap = 0;    // bytes of the device allocation (its cache size class)
 };
 
 struct rt_prof_rec {
@@ -34,12 +37,16 @@ struct rt_ctx {
   // Device flags written by kernels: [0] label out of range, [1] non-finite
   // gradient.  Zeroed by a fill kernel, read back by the blocking readers.
   int* d_flags = nullptr;
-  // Grow-only device scratch for ops that need temporaries (colsum stage 1).
+  // Grow-only device scratch for ops that need temporaries (colsum stage 1,
+  // sum partials, loss terms, argmax predictions); see ensure_scratch.
   float* scratch = nullptr;
   size_t scratch_elems = 0;
+  // Freed buffer allocations by size class, reused in stream order.
+  std::unordered_map<size_t, std::vector<void*>> pool;
+  size_t pool_bytes = 0;
   bool profiling = false;
   // Children freed by rt_close if the caller has not freed them.
-  std::vector<rt_buf*> bufs;
+  std::unordered_set<rt_buf*> bufs;
   std::vector<rt_mlp*> mlps;
   std::vector<rt_prof_rec> prof;
   std::vector<hipEvent_t> event_pool;
@@ -54,6 +61,20 @@ void mlp_release(rt_mlp* p);  // frees the plan's device memory and the struct
 size_t dtype_size(rt_dtype d);
 int fail(rt_ctx* c, int code, const char* fmt, ...);
 int hip_fail(rt_ctx* c, hipError_t e, const char* what);
+// Makes c->scratch hold at least elems floats (grow-only; waits for queued
+// work before replacing a smaller one).
+int ensure_scratch(rt_ctx* c, size_t elems);
+
+#define CHECK_CTX(c)                           \
+  do {                                         \
+    if ((c) == nullptr) return RT_ERR_INVALID; \
+  } while (0)
+
+#define HIP_TRY(c, expr, what)                                  \
+  do {                                                          \
+    hipError_t _e = (expr);                                     \
+    if (_e != hipSuccess) return ::rt::hip_fail((c), _e, what); \
+  } while (0)
 
 // Brackets one kernel launch with HIP events when profiling is on.
 class Launch {
@@ -160,6 +181,26 @@ constexpr int kMaxOptTensors = 24;
 hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const OptParams& p);
 // Sets *flag = 1 if any of the n floats of any tensor is not finite.
 hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag);
+
+// ---------------------------------------------------------------- tensor ops (tensor_ops.hip)
+hipError_t unary_launch(hipStream_t s, int op, float k, const float* x, float* y, long long n);
+hipError_t unary_vjp_launch(hipStream_t s, int op, float k, const float* g, const float* x, const float* y, float* dx,
+                            long long n);
+// out[l] = a[ia] op b[ib] over the output shape (rank 1..4); sa / sb are the
+// operands' strides in the output index space (0 on broadcast axes).
+hipError_t binary_launch(hipStream_t s, int op, const float* a, const long long* sa, const float* b,
+                         const long long* sb, float* out, const long long* shape, int rank);
+// tshape: same rank as gshape, each axis equal to g's or 1.
+hipError_t reduce_to_launch(hipStream_t s, const float* g, const long long* gshape, int grank, float* out,
+                            const long long* tshape);
+size_t sum_scratch_elems(long long n);
+hipError_t sum_all_launch(hipStream_t s, const float* x, long long n, float div, float* out, float* scratch);
+hipError_t scalar_fill_launch(hipStream_t s, const float* scalar, float div, const float* x, float* out, long long n);
+hipError_t softmax_rows_launch(hipStream_t s, const float* z, float* y, long long rows, long long cols);
+hipError_t softmax_rows_vjp_launch(hipStream_t s, const float* sm, const float* g, float* dx, long long rows,
+                                   long long cols);
+hipError_t loss_terms_launch(hipStream_t s, int kind, const float* p, const float* y, float* term, float* dir,
+                             long long n);
 
 // f32 powi as rtensor's Adam computes β^t (square-and-multiply).
 float powi_f32(float a, int b);

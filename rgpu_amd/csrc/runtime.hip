@@ -44,6 +44,18 @@ int hip_fail(rt_ctx* c, hipError_t e, const char* what) {
   return fail(c, e == hipErrorOutOfMemory ? RT_ERR_OOM : RT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+int ensure_scratch(rt_ctx* c, size_t elems) {
+  if (elems <= c->scratch_elems) return RT_OK;
+  // Earlier work may still read the old scratch.
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "scratch sync");
+  if (c->scratch) hipFree(c->scratch);
+  c->scratch = nullptr;
+  c->scratch_elems = 0;
+  HIP_TRY(c, hipMalloc((void**)&c->scratch, elems * sizeof(float)), "scratch");
+  c->scratch_elems = elems;
+  return RT_OK;
+}
+
 Launch::Launch(rt_ctx* c, const char* label) : c_(c), label_(label) {
   if (!c_->profiling) return;
   if (c_->event_pool.empty()) {
@@ -77,17 +89,6 @@ Launch::~Launch() {
 using namespace rt;
 
 static std::string g_open_err;
-
-#define CHECK_CTX(c)                                       \
-  do {                                                     \
-    if ((c) == nullptr) return RT_ERR_INVALID;             \
-  } while (0)
-
-#define HIP_TRY(c, expr, what)                             \
-  do {                                                     \
-    hipError_t _e = (expr);                                \
-    if (_e != hipSuccess) return hip_fail((c), _e, what);  \
-  } while (0)
 
 static bool is_half(rt_dtype d) { return d == RT_BF16 || d == RT_F16; }
 static size_t cols_of(const rt_buf* b) { return b->rank >= 2 ? b->shape[b->rank - 1] : b->n; }
@@ -156,6 +157,9 @@ int rt_close(rt_ctx* c) {
     delete b;
   }
   c->bufs.clear();
+  for (auto& kv : c->pool)
+    for (void* ptr : kv.second) hipFree(ptr);
+  c->pool.clear();
   for (auto& r : c->prof) {
     hipEventDestroy(r.e0);
     hipEventDestroy(r.e1);
@@ -193,6 +197,53 @@ int rt_sync(rt_ctx* c) {
   return RT_OK;
 }
 
+// Size classes of the buffer cache: 256-byte steps up to 1 MiB, then 1 MiB
+// steps.  Cached bytes above kPoolMax are given back instead of kept.
+static size_t size_class(size_t bytes) {
+  constexpr size_t kMiB = size_t(1) << 20;
+  if (bytes <= kMiB) return (bytes + 255) & ~size_t(255);
+  return (bytes + kMiB - 1) & ~(kMiB - 1);
+}
+static constexpr size_t kPoolMax = size_t(16) << 30;
+
+static void pool_trim(rt_ctx* c) {
+  hipStreamSynchronize(c->stream);
+  for (auto& kv : c->pool)
+    for (void* ptr : kv.second) hipFree(ptr);
+  c->pool.clear();
+  c->pool_bytes = 0;
+}
+
+static hipError_t pool_alloc(rt_ctx* c, size_t cap, void** ptr) {
+  auto it = c->pool.find(cap);
+  if (it != c->pool.end() && !it->second.empty()) {
+    *ptr = it->second.back();
+    it->second.pop_back();
+    c->pool_bytes -= cap;
+    return hipSuccess;
+  }
+  hipError_t e = hipMalloc(ptr, cap);
+  if (e == hipErrorOutOfMemory && c->pool_bytes > 0) {
+    (void)hipGetLastError();
+    pool_trim(c);
+    e = hipMalloc(ptr, cap);
+  }
+  return e;
+}
+
+// Returns an allocation to the cache.  Work already enqueued may still use
+// it; anything that reuses it is enqueued later on the same stream.
+static void pool_release(rt_ctx* c, void* ptr, size_t cap) {
+  if (ptr == nullptr) return;
+  if (c->pool_bytes + cap > kPoolMax) {
+    hipStreamSynchronize(c->stream);
+    hipFree(ptr);
+    return;
+  }
+  c->pool[cap].push_back(ptr);
+  c->pool_bytes += cap;
+}
+
 static int make_buf(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out) {
   if (out == nullptr || (rank > 0 && shape == nullptr) || rank < 0 || rank > 4)
     return fail(c, RT_ERR_INVALID, "bad shape arguments");
@@ -208,21 +259,24 @@ static int make_buf(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt
   b->n = n;
   b->bytes = n * dtype_size(dtype);
   if (b->bytes > 0) {
-    // Whole 4-byte words, so zero fills never need a byte memset.
-    hipError_t e = hipMalloc(&b->ptr, (b->bytes + 3) / 4 * 4);
+    // Whole 256-byte granules, so fills and vector loads never need a tail.
+    b->cap = size_class(b->bytes);
+    hipError_t e = pool_alloc(c, b->cap, &b->ptr);
     if (e != hipSuccess) {
       delete b;
       return hip_fail(c, e, "hipMalloc");
     }
   }
-  c->bufs.push_back(b);
+  c->bufs.insert(b);
   *out = b;
   return RT_OK;
 }
 
-static void forget_buf(rt_ctx* c, rt_buf* b) {
-  auto it = std::find(c->bufs.begin(), c->bufs.end(), b);
-  if (it != c->bufs.end()) c->bufs.erase(it);
+// Undoes make_buf for a buffer whose initialisation failed.
+static void drop_buf(rt_ctx* c, rt_buf* b) {
+  c->bufs.erase(b);
+  pool_release(c, b->ptr, b->cap);
+  delete b;
 }
 
 int rt_zeros(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out) {
@@ -234,16 +288,18 @@ int rt_zeros(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** 
     // Zero fill with a kernel, not a memset node (graph-capture safe).
     size_t words = (b->bytes + 3) / 4;
     hipError_t e = fill_i32_launch(c->stream, static_cast<int*>(b->ptr), 0, words);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
-      forget_buf(c, b);
-      hipFree(b->ptr);
-      delete b;
+      drop_buf(c, b);
       *out = nullptr;
       return hip_fail(c, e, "zero fill");
     }
   }
   return RT_OK;
+}
+
+int rt_empty(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt_buf** out) {
+  CHECK_CTX(c);
+  return make_buf(c, dtype, shape, rank, out);
 }
 
 int rt_upload(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, const void* host, rt_buf** out) {
@@ -253,18 +309,15 @@ int rt_upload(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, const vo
   rt_buf* b = *out;
   if (b->bytes > 0) {
     if (host == nullptr) {
-      forget_buf(c, b);
-      hipFree(b->ptr);
-      delete b;
+      drop_buf(c, b);
       *out = nullptr;
       return fail(c, RT_ERR_INVALID, "null host pointer");
     }
     hipError_t e = hipMemcpyAsync(b->ptr, host, b->bytes, hipMemcpyHostToDevice, c->stream);
+    // The host buffer is caller-owned and may be reused on return.
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
-      forget_buf(c, b);
-      hipFree(b->ptr);
-      delete b;
+      drop_buf(c, b);
       *out = nullptr;
       return hip_fail(c, e, "upload");
     }
@@ -296,13 +349,8 @@ int rt_write(rt_ctx* c, rt_buf* b, const void* host, size_t bytes) {
 int rt_free(rt_ctx* c, rt_buf* b) {
   CHECK_CTX(c);
   if (b == nullptr) return RT_OK;
-  if (std::find(c->bufs.begin(), c->bufs.end(), b) == c->bufs.end())
-    return fail(c, RT_ERR_INVALID, "buffer does not belong to this context");
-  forget_buf(c, b);
-  // Work already enqueued may still read the buffer.
-  hipStreamSynchronize(c->stream);
-  if (b->ptr) hipFree(b->ptr);
-  delete b;
+  if (c->bufs.find(b) == c->bufs.end()) return fail(c, RT_ERR_INVALID, "buffer does not belong to this context");
+  drop_buf(c, b);
   return RT_OK;
 }
 
@@ -489,16 +537,8 @@ int rt_colsum(rt_ctx* c, const rt_buf* src, rt_buf* dst) {
   size_t R = src->shape[0], Cc = src->shape[1];
   if (dst->dtype != RT_F32 || dst->n != Cc) return fail(c, RT_ERR_SHAPE, "colsum target must be f32 [1,%zu]", Cc);
   if (src->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "colsum of u32");
-  size_t se = colsum_scratch_elems((int)R, (int)Cc);
-  if (se > c->scratch_elems) {
-    // Grow the context scratch; earlier work may still read the old one.
-    HIP_TRY(c, hipStreamSynchronize(c->stream), "scratch sync");
-    if (c->scratch) hipFree(c->scratch);
-    c->scratch = nullptr;
-    c->scratch_elems = 0;
-    HIP_TRY(c, hipMalloc((void**)&c->scratch, se * sizeof(float)), "colsum scratch");
-    c->scratch_elems = se;
-  }
+  int rc = ensure_scratch(c, colsum_scratch_elems((int)R, (int)Cc));
+  if (rc) return rc;
   Launch L(c, "colsum");
   HIP_TRY(c, colsum_launch(c->stream, src->ptr, src->dtype, (int)R, (int)Cc, static_cast<float*>(dst->ptr), c->scratch,
                            c->scratch_elems),
@@ -591,13 +631,8 @@ int rt_accuracy(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, float* ou
   if (Cc == 0) return fail(c, RT_ERR_SHAPE, "zero classes");
   if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "too large");
   // Predictions in the context scratch (grow-only), then compared on the host.
-  if (c->scratch_elems < B) {
-    if (c->scratch) HIP_TRY(c, hipFree(c->scratch), "scratch free");
-    c->scratch = nullptr;
-    c->scratch_elems = 0;
-    HIP_TRY(c, hipMalloc(&c->scratch, B * sizeof(float)), "scratch");
-    c->scratch_elems = B;
-  }
+  int rc = ensure_scratch(c, B);
+  if (rc) return rc;
   uint32_t* pred = reinterpret_cast<uint32_t*>(c->scratch);
   {
     Launch L(c, "argmax");

@@ -43,6 +43,11 @@ NN, TN, NT = 0, 1, 2
 EPI_NONE, EPI_BIAS, EPI_BIAS_RELU, EPI_RELU_MASK = 0, 1, 2, 3
 OPT_ADAM, OPT_SGD = 0, 1
 PREC_F32, PREC_BF16 = 0, 1
+# rt_unary_op, rt_binary_op, rt_loss_kind
+UNARY = {"scale": 0, "offset": 1, "neg": 2, "square": 3, "sqrt": 4, "exp": 5, "ln": 6, "relu": 7,
+         "leaky_relu": 8, "sigmoid": 9, "tanh": 10}
+BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3}
+LOSS_MAE, LOSS_SOFTMAX_XENT, LOSS_BCE = 1, 2, 3
 
 STATUS = {0: "RT_OK", 1: "RT_ERR_NO_DEVICE", 2: "RT_ERR_INVALID", 3: "RT_ERR_SHAPE", 4: "RT_ERR_DTYPE",
           5: "RT_ERR_OOM", 6: "RT_ERR_LABEL", 7: "RT_ERR_HIP", 8: "RT_ERR_OVERFLOW"}
@@ -98,6 +103,16 @@ SIGNATURES = {
                                              C.c_int, C.c_int]),
     "rt_argmax_rows": (C.c_int, [_VP, _VP, _VP]),
     "rt_accuracy": (C.c_int, [_VP, _VP, _VP, C.POINTER(C.c_float)]),
+    "rt_map": (C.c_int, [_VP, C.c_int, C.c_float, _VP, _VP]),
+    "rt_map_vjp": (C.c_int, [_VP, C.c_int, C.c_float, _VP, _VP, _VP, _VP]),
+    "rt_zip": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP]),
+    "rt_reduce_to": (C.c_int, [_VP, _VP, _VP]),
+    "rt_sum_all": (C.c_int, [_VP, _VP, C.c_float, _VP]),
+    "rt_fill_scaled": (C.c_int, [_VP, _VP, C.c_float, _VP, _VP]),
+    "rt_softmax_rows": (C.c_int, [_VP, _VP, _VP]),
+    "rt_softmax_rows_vjp": (C.c_int, [_VP, _VP, _VP, _VP]),
+    "rt_loss": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, _VP]),
+    "rt_empty": (C.c_int, [_VP, C.c_int, _SZP, C.c_int, C.POINTER(_VP)]),
 }
 
 
@@ -223,6 +238,14 @@ class Gpu:
         self._call("rt_zeros", self._h, dtype, arr, len(shape), C.byref(h))
         return GpuTensor(self, h.value, shape, dtype)
 
+    def empty(self, shape, dtype: int = F32) -> GpuTensor:
+        """A buffer whose contents are undefined, for outputs written whole."""
+        shape = tuple(int(s) for s in shape)
+        arr = (C.c_size_t * max(len(shape), 1))(*shape)
+        h = C.c_void_p()
+        self._call("rt_empty", self._h, dtype, arr, len(shape), C.byref(h))
+        return GpuTensor(self, h.value, shape, dtype)
+
     def upload(self, a, dtype: Optional[int] = None) -> GpuTensor:
         """Upload a host array.  dtype BF16 takes f32 values (rounded to
         nearest even) or uint16 bit patterns; F16 takes anything numpy can
@@ -324,6 +347,45 @@ class Gpu:
         v = C.c_float()
         self._call("rt_accuracy", self._h, logits.handle, labels.handle, C.byref(v))
         return v.value
+
+    # --------------------------------------------------------------- tensor ops
+    def map(self, op: str, x, y, k: float = 0.0):
+        """Tensor::map with the forward closure of ops.rs's ``op`` (y = f(x))."""
+        self._call("rt_map", self._h, UNARY[op], k, x.handle, y.handle)
+
+    def map_vjp(self, op: str, g, x, y, dx, k: float = 0.0):
+        """The VJP closure of ``op`` (ops.rs:132-227); x / y may be None when unused."""
+        self._call("rt_map_vjp", self._h, UNARY[op], k, g.handle, x.handle if x is not None else None,
+                   y.handle if y is not None else None, dx.handle)
+
+    def zip(self, op: str, a, b, out):
+        """Tensor::zip (tensor.rs:183-246) with broadcasting; op in add/sub/mul/div."""
+        self._call("rt_zip", self._h, BINARY[op], a.handle, b.handle, out.handle)
+
+    def reduce_to(self, g, out):
+        """Tensor::reduce_to (tensor.rs:399-438) onto out's shape."""
+        self._call("rt_reduce_to", self._h, g.handle, out.handle)
+
+    def sum_all(self, x, out, div: float = 1.0):
+        """out[0] = sum_all(x) / div (tensor.rs:279-286)."""
+        self._call("rt_sum_all", self._h, x.handle, div, out.handle)
+
+    def fill_scaled(self, s, out, div: float = 1.0, x=None):
+        """out = x * (s / div), or Tensor::full(s / div) when x is None."""
+        self._call("rt_fill_scaled", self._h, s.handle, div, x.handle if x is not None else None, out.handle)
+
+    def softmax_rows(self, z, y):
+        """Tensor::softmax_rows (tensor.rs:455-472)."""
+        self._call("rt_softmax_rows", self._h, z.handle, y.handle)
+
+    def softmax_rows_vjp(self, s, g, dx):
+        """softmax's VJP (ops.rs:291-309): dx = s * (g - rowsum(g * s))."""
+        self._call("rt_softmax_rows_vjp", self._h, s.handle, g.handle, dx.handle)
+
+    def loss(self, kind: int, p, y, value, dir_=None):
+        """Loss value (total / batch) and unscaled gradient direction (losses.rs)."""
+        self._call("rt_loss", self._h, kind, p.handle, y.handle if y is not None else None, value.handle,
+                   dir_.handle if dir_ is not None else None)
 
     # --------------------------------------------------------------- profiling
     def profile(self, on: bool) -> None:
