@@ -1,6 +1,6 @@
 """Benchmark of the MLP training step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only all|step|bwd|splitk|mixed]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only all|step|bwd|splitk|mixed|tape]
 
 Workload (one "step"): MLP 512->1024(ReLU)->1024(ReLU)->10, f32, batch 2048,
 softmax cross-entropy, Adam(1e-3, 0.9, 0.999, 1e-8): forward, backward and the
@@ -17,12 +17,16 @@ better).  Next to it:
                 the HBM roofline
   mixed_mlp     8 x 4096 ReLU MLP -> 1000 classes, batch 4096, bf16 with f32
                 master weights, loss scale 1024, Adam: ms/step and TFLOP/s
+  tape_mlp      examples/bench_grande.rs (N 4096, D 128, H 512, minibatch
+                256, Adam) trained through the device autodiff tape, one
+                HIP launch per recorded op, against the oracle's CPU tape
   cpu_baseline  the CPU oracle (C++ restatement of rtensor's single-threaded
                 CPU path) timed on a bounded sample of the same workload
 """
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import platform
@@ -213,6 +217,111 @@ def bench_mixed(gpu, G, steps=20, warmup=3):
             "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "final_loss": round(float(loss), 4)}
 
 
+# examples/bench_grande.rs: N samples of D features, two ReLU layers of H,
+# 10 classes, minibatches of LOTE, Adam(1e-3), softmax cross-entropy.
+TAPE_N, TAPE_D, TAPE_H, TAPE_LOTE, TAPE_C = 4096, 128, 512, 256, 10
+
+
+def tape_data():
+    """bench_grande.rs:27-35: x[i][j] = sin(0.01 i + 0.03 j) (f32), label i % 10."""
+    i = np.arange(TAPE_N, dtype=np.float32)[:, None]
+    j = np.arange(TAPE_D, dtype=np.float32)[None, :]
+    x = np.sin(i * np.float32(0.01) + j * np.float32(0.03)).astype(np.float32)
+    y = np.zeros((TAPE_N, TAPE_C), np.float32)
+    y[np.arange(TAPE_N), np.arange(TAPE_N) % TAPE_C] = 1.0
+    return x, y
+
+
+def tape_step_flops(rows):
+    """bench_grande.rs:63-65: (D*H + H*H + H*C) MACs per sample, x3 fwd+bwd, x2."""
+    return (TAPE_D * TAPE_H + TAPE_H * TAPE_H + TAPE_H * TAPE_C) * 3 * 2 * rows
+
+
+def bench_tape(gpu, G, epochs=3):
+    """bench_grande.rs on the device tape: a Sequential model recorded op by op
+    (matmul, broadcast add, relu, softmax-xent) and Adam, every op a HIP
+    launch; minibatches resident in HBM before the timed epochs."""
+    from rgpu_amd import autograd as A
+
+    x, y = tape_data()
+    rng = np.random.default_rng(7)
+
+    def glorot(d, h):
+        lim = np.sqrt(6.0 / (d + h))
+        return rng.uniform(-lim, lim, (d, h)).astype(np.float32)
+
+    dims = [TAPE_D, TAPE_H, TAPE_H, TAPE_C]
+    acts = ["relu", "relu", "linear"]
+    model = A.Sequential([A.Dense(gpu, dims[k], dims[k + 1], acts[k], weights=glorot(dims[k], dims[k + 1]))
+                          for k in range(3)])
+    params = model.params()
+    opt = A.Adam(1e-3)
+    batches = [(gpu.upload(x[i:i + TAPE_LOTE]), gpu.upload(y[i:i + TAPE_LOTE]))
+               for i in range(0, TAPE_N, TAPE_LOTE)]
+
+    def epoch():
+        loss = None
+        for bx, by in batches:
+            t = A.Tape(gpu)
+            loss = A.softmax_cross_entropy(model.forward(t.constant(bx)), by)
+            opt.step(params, loss.backward())
+        return loss
+
+    epoch()  # warm-up
+    gpu.sync()
+    t0 = time.perf_counter()
+    for _ in range(epochs):
+        loss = epoch()
+    gpu.sync()
+    wall = time.perf_counter() - t0
+    steps = epochs * len(batches)
+    # device time of the same work, and the per-kernel split, in one more epoch
+    gpu.timer_begin()
+    epoch()
+    dev_ms = gpu.timer_end() / len(batches)
+    gpu.profile_reset()
+    gpu.profile(True)
+    epoch()
+    gpu.sync()
+    prof = gpu.perfilar()
+    gpu.profile(False)
+    flops = tape_step_flops(TAPE_LOTE)
+    ms = wall / steps * 1e3
+    kern = sorted(((n, c, t) for n, c, t in prof), key=lambda r: -r[2])
+    return {"config": f"bench_grande: N={TAPE_N} D={TAPE_D} H={TAPE_H} lote={TAPE_LOTE}, Sequential "
+                      "Dense(relu) x2 + Dense(linear) -> softmax-xent, Adam(1e-3), device tape",
+            "steps": steps, "ms_per_step": round(ms, 4), "device_ms_per_step": round(dev_ms, 4),
+            "gflops": round(flops / (ms * 1e-3) / 1e9, 1), "launches_per_step": sum(c for _, c, _ in prof) // len(batches),
+            "final_loss": round(loss.item(), 4),
+            "kernels_ms_per_step": {n: round(t / len(batches), 4) for n, _, t in kern[:8]}}
+
+
+def cpu_tape_baseline(budget_s=10.0):
+    """bench_grande.rs on the oracle's tape (the reference's CPU path), 1 thread."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    x, y = tape_data()
+    rng = O.Rng(7)
+    layers = [O.Dense(TAPE_D, TAPE_H, "relu", rng), O.Dense(TAPE_H, TAPE_H, "relu", rng),
+              O.Dense(TAPE_H, TAPE_C, "linear", rng)]
+    model = O.Sequential(layers)
+    params = model.params()
+    opt = O.Optimizer("adam", 1e-3)
+    t0 = time.perf_counter()
+    n = 0
+    for i in itertools.cycle(range(0, TAPE_N, TAPE_LOTE)):
+        t = O.Tape()
+        O.loss("softmax_cross_entropy", model.forward(t.constant(x[i:i + TAPE_LOTE])), y[i:i + TAPE_LOTE]).backward()
+        opt.step(params, t)
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 48:
+            break
+    ms = (time.perf_counter() - t0) / n * 1e3
+    return {"value": round(ms, 3), "unit": "ms/step", "cores": 1, "kind": "port",
+            "sample": f"{n} minibatch steps of bench_grande (lote {TAPE_LOTE}) on the oracle tape, 1 thread"}
+
+
 def bench_copy(gpu, G, mib=256, reps=5):
     """A plain device copy of known size (f32 -> f32 through the convert
     kernel): reads and writes exactly mib MiB per launch.  Used to calibrate
@@ -266,7 +375,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy", "tape"], default="all",
                     help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -277,8 +386,9 @@ def main():
     from rgpu_amd import gpu as G
 
     gpu = G.Gpu(0)
-    if args.only in ("bwd", "splitk", "mixed", "copy"):
-        fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed, "copy": bench_copy}[args.only]
+    if args.only in ("bwd", "splitk", "mixed", "copy", "tape"):
+        fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed, "copy": bench_copy,
+              "tape": bench_tape}[args.only]
         print(json.dumps({args.only: fn(gpu, G)}), flush=True)
         return
     wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
@@ -331,10 +441,15 @@ def main():
         out["bwd_gemm"] = bench_bwd_gemm(gpu, G)
         out["splitk_dw"] = bench_splitk(gpu, G)
         out["mixed_mlp"] = bench_mixed(gpu, G)
+        out["tape_mlp"] = bench_tape(gpu, G)
     if not args.no_cpu:
         cb = cpu_baseline()
         out["cpu_baseline"] = cb
         out["speedup_vs_cpu"] = round(cb["value"] / ms, 1)
+        if "tape_mlp" in out:
+            ct = cpu_tape_baseline()
+            out["tape_mlp"]["cpu_baseline"] = ct
+            out["tape_mlp"]["speedup_vs_cpu"] = round(ct["value"] / out["tape_mlp"]["ms_per_step"], 1)
     print(json.dumps(out), flush=True)
 
 

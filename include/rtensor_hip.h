@@ -138,6 +138,14 @@ int rt_adam(rt_ctx* ctx, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, f
             float beta2, float eps, int t);
 /* Sgd::step (optim.rs:80-114); velocity may be NULL when momentum == 0. */
 int rt_sgd(rt_ctx* ctx, rt_buf* theta, rt_buf* velocity, const rt_buf* g, float lr, float momentum);
+/* Adam::step / Sgd::step over a whole parameter list (optim.rs:80-114,
+ * 162-198: the loop over params), as one launch per 24 tensors instead of
+ * one per tensor.  Arrays of n buffers; for SGD without momentum velocity
+ * may be NULL.  Arithmetic identical to rt_adam / rt_sgd. */
+int rt_adam_many(rt_ctx* ctx, int n, rt_buf* const* theta, rt_buf* const* m, rt_buf* const* v,
+                 const rt_buf* const* g, float lr, float beta1, float beta2, float eps, int t);
+int rt_sgd_many(rt_ctx* ctx, int n, rt_buf* const* theta, rt_buf* const* velocity, const rt_buf* const* g,
+                float lr, float momentum);
 
 /* ------------------------------------------------------------- model */
 

@@ -482,6 +482,25 @@ def accuracy(logits: Union[Var, GpuTensor], labels) -> float:
 
 
 # ------------------------------------------------------------------ optimizers
+def _live_groups(params: Sequence[Param], grads: Grads):
+    """The parameters that have a gradient, in order, cut into runs without a
+    repeated parameter: the reference updates a parameter listed twice twice,
+    one after the other, and one launch cannot."""
+    groups, cur, seen = [], [], set()
+    for p in params:
+        g = grads.of(p)
+        if g is None:
+            continue
+        if p.id in seen:
+            groups.append(cur)
+            cur, seen = [], set()
+        cur.append((p, g))
+        seen.add(p.id)
+    if cur:
+        groups.append(cur)
+    return groups
+
+
 class Sgd:
     """optim.rs:64-114: θ −= α g, or v = μ v + α g; θ −= v."""
 
@@ -494,17 +513,19 @@ class Sgd:
         return cls(lr, momentum)
 
     def step(self, params: Sequence[Param], grads: Grads) -> None:
-        for p in params:
-            g = grads.of(p)
-            if g is None:
-                continue
+        for live in _live_groups(params, grads):
+            gpu = live[0][0].gpu
+            thetas, gs = [p.tensor for p, _ in live], [g for _, g in live]
             if self.momentum == 0.0:
-                p.gpu.sgd(p.tensor, g, self.lr)
-            else:
+                gpu.sgd_many(thetas, gs, self.lr)
+                continue
+            vel = []
+            for p, _ in live:
                 v = self.velocity.get(p.id)
                 if v is None:
                     v = self.velocity[p.id] = p.gpu.zeros(p.shape)
-                p.gpu.sgd(p.tensor, g, self.lr, self.momentum, v)
+                vel.append(v)
+            gpu.sgd_many(thetas, gs, self.lr, self.momentum, vel)
 
 
 class Adam:
@@ -522,15 +543,14 @@ class Adam:
 
     def step(self, params: Sequence[Param], grads: Grads) -> None:
         self.t += 1
-        for p in params:
-            g = grads.of(p)
-            if g is None:
-                continue
-            m = self.m.get(p.id)
-            if m is None:
-                m = self.m[p.id] = p.gpu.zeros(p.shape)
-                self.v[p.id] = p.gpu.zeros(p.shape)
-            p.gpu.adam(p.tensor, m, self.v[p.id], g, self.lr, (self.beta1, self.beta2), self.t, self.eps)
+        for live in _live_groups(params, grads):
+            for p, _ in live:
+                if p.id not in self.m:
+                    self.m[p.id] = p.gpu.zeros(p.shape)
+                    self.v[p.id] = p.gpu.zeros(p.shape)
+            live[0][0].gpu.adam_many([p.tensor for p, _ in live], [self.m[p.id] for p, _ in live],
+                                     [self.v[p.id] for p, _ in live], [g for _, g in live], self.lr,
+                                     (self.beta1, self.beta2), self.t, self.eps)
 
 
 # ------------------------------------------------------------------ layers

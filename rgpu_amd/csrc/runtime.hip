@@ -648,16 +648,33 @@ int rt_accuracy(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, float* ou
   return RT_OK;
 }
 
-int rt_adam(rt_ctx* c, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, float lr, float beta1, float beta2,
-            float eps, int t) {
+// One launch per kMaxOptTensors tensors of the list.
+static int launch_opt_list(rt_ctx* c, const std::vector<OptTensor>& ts, const OptParams& P) {
+  for (size_t i = 0; i < ts.size(); i += kMaxOptTensors) {
+    const int nt = (int)std::min<size_t>(kMaxOptTensors, ts.size() - i);
+    Launch L(c, "optimizer");
+    HIP_TRY(c, optimizer_launch(c->stream, ts.data() + i, nt, P), "optimizer");
+  }
+  return RT_OK;
+}
+
+int rt_adam_many(rt_ctx* c, int n, rt_buf* const* theta, rt_buf* const* m, rt_buf* const* v, const rt_buf* const* g,
+                 float lr, float beta1, float beta2, float eps, int t) {
   CHECK_CTX(c);
-  if (!theta || !m || !v || !g) return fail(c, RT_ERR_INVALID, "null buffer");
-  if (theta->dtype != RT_F32 || m->dtype != RT_F32 || v->dtype != RT_F32 || g->dtype != RT_F32)
-    return fail(c, RT_ERR_DTYPE, "adam is f32");
-  if (m->n != theta->n || v->n != theta->n || g->n != theta->n) return fail(c, RT_ERR_SHAPE, "adam: sizes differ");
+  if (n < 0 || (n > 0 && (!theta || !m || !v || !g))) return fail(c, RT_ERR_INVALID, "null tensor list");
   if (t < 1) return fail(c, RT_ERR_INVALID, "adam step t must be >= 1");
-  OptTensor T{static_cast<float*>(theta->ptr), static_cast<const float*>(g->ptr), static_cast<float*>(m->ptr),
-              static_cast<float*>(v->ptr), nullptr, theta->n};
+  std::vector<OptTensor> ts;
+  ts.reserve(n);
+  for (int i = 0; i < n; ++i) {
+    if (!theta[i] || !m[i] || !v[i] || !g[i]) return fail(c, RT_ERR_INVALID, "null buffer (tensor %d)", i);
+    if (theta[i]->dtype != RT_F32 || m[i]->dtype != RT_F32 || v[i]->dtype != RT_F32 || g[i]->dtype != RT_F32)
+      return fail(c, RT_ERR_DTYPE, "adam is f32 (tensor %d)", i);
+    const size_t len = theta[i]->n;
+    if (m[i]->n != len || v[i]->n != len || g[i]->n != len) return fail(c, RT_ERR_SHAPE, "adam: sizes differ (tensor %d)", i);
+    if (len == 0) continue;
+    ts.push_back(OptTensor{static_cast<float*>(theta[i]->ptr), static_cast<const float*>(g[i]->ptr),
+                           static_cast<float*>(m[i]->ptr), static_cast<float*>(v[i]->ptr), nullptr, len});
+  }
   OptParams P;
   P.kind = 0;
   P.lr = lr;
@@ -667,27 +684,42 @@ int rt_adam(rt_ctx* c, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, flo
   float c1 = 1.0f - powi_f32(beta1, t), c2 = 1.0f - powi_f32(beta2, t);
   P.inv_c1 = 1.0f / c1;
   P.inv_c2 = 1.0f / c2;
-  Launch L(c, "optimizer");
-  HIP_TRY(c, optimizer_launch(c->stream, &T, 1, P), "adam");
-  return RT_OK;
+  return launch_opt_list(c, ts, P);
 }
 
-int rt_sgd(rt_ctx* c, rt_buf* theta, rt_buf* velocity, const rt_buf* g, float lr, float momentum) {
+int rt_adam(rt_ctx* c, rt_buf* theta, rt_buf* m, rt_buf* v, const rt_buf* g, float lr, float beta1, float beta2,
+            float eps, int t) {
+  return rt_adam_many(c, 1, &theta, &m, &v, &g, lr, beta1, beta2, eps, t);
+}
+
+int rt_sgd_many(rt_ctx* c, int n, rt_buf* const* theta, rt_buf* const* velocity, const rt_buf* const* g, float lr,
+                float momentum) {
   CHECK_CTX(c);
-  if (!theta || !g) return fail(c, RT_ERR_INVALID, "null buffer");
-  if (theta->dtype != RT_F32 || g->dtype != RT_F32) return fail(c, RT_ERR_DTYPE, "sgd is f32");
-  if (g->n != theta->n) return fail(c, RT_ERR_SHAPE, "sgd: sizes differ");
-  if (momentum != 0.0f && (velocity == nullptr || velocity->n != theta->n || velocity->dtype != RT_F32))
-    return fail(c, RT_ERR_INVALID, "sgd with momentum needs an f32 velocity buffer");
-  OptTensor T{static_cast<float*>(theta->ptr), static_cast<const float*>(g->ptr),
-              velocity ? static_cast<float*>(velocity->ptr) : nullptr, nullptr, nullptr, theta->n};
+  if (n < 0 || (n > 0 && (!theta || !g))) return fail(c, RT_ERR_INVALID, "null tensor list");
+  if (momentum != 0.0f && n > 0 && !velocity) return fail(c, RT_ERR_INVALID, "sgd with momentum needs velocities");
+  std::vector<OptTensor> ts;
+  ts.reserve(n);
+  for (int i = 0; i < n; ++i) {
+    if (!theta[i] || !g[i]) return fail(c, RT_ERR_INVALID, "null buffer (tensor %d)", i);
+    if (theta[i]->dtype != RT_F32 || g[i]->dtype != RT_F32) return fail(c, RT_ERR_DTYPE, "sgd is f32 (tensor %d)", i);
+    const size_t len = theta[i]->n;
+    if (g[i]->n != len) return fail(c, RT_ERR_SHAPE, "sgd: sizes differ (tensor %d)", i);
+    rt_buf* vel = momentum != 0.0f ? velocity[i] : nullptr;
+    if (momentum != 0.0f && (vel == nullptr || vel->n != len || vel->dtype != RT_F32))
+      return fail(c, RT_ERR_INVALID, "sgd with momentum needs an f32 velocity buffer (tensor %d)", i);
+    if (len == 0) continue;
+    ts.push_back(OptTensor{static_cast<float*>(theta[i]->ptr), static_cast<const float*>(g[i]->ptr),
+                           vel ? static_cast<float*>(vel->ptr) : nullptr, nullptr, nullptr, len});
+  }
   OptParams P;
   P.kind = 1;
   P.lr = lr;
   P.momentum = momentum;
-  Launch L(c, "optimizer");
-  HIP_TRY(c, optimizer_launch(c->stream, &T, 1, P), "sgd");
-  return RT_OK;
+  return launch_opt_list(c, ts, P);
+}
+
+int rt_sgd(rt_ctx* c, rt_buf* theta, rt_buf* velocity, const rt_buf* g, float lr, float momentum) {
+  return rt_sgd_many(c, 1, &theta, &velocity, &g, lr, momentum);
 }
 
 // ------------------------------------------------------------------ profiling

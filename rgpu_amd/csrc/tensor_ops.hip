@@ -132,12 +132,33 @@ __global__ __launch_bounds__(256) void reduce_to_kernel(const float* __restrict_
       base += (rem % r.keep_n[ax]) * r.keep_s[ax];
       rem /= r.keep_n[ax];
     }
+    // The adds form one dependent chain.  Loads go out in batches of kBatch,
+    // the next batch issued before the current one is added, so the chain
+    // rarely waits on memory.
+    constexpr int kBatch = 32;
+    const long long n3 = r.red_n[3], s3 = r.red_s[3];
     float acc = 0.0f;
     for (long long i0 = 0; i0 < r.red_n[0]; ++i0)
       for (long long i1 = 0; i1 < r.red_n[1]; ++i1)
         for (long long i2 = 0; i2 < r.red_n[2]; ++i2) {
           const float* p = g + base + i0 * r.red_s[0] + i1 * r.red_s[1] + i2 * r.red_s[2];
-          for (long long i3 = 0; i3 < r.red_n[3]; ++i3) acc += p[i3 * r.red_s[3]];
+          long long i3 = 0;
+          if (n3 >= kBatch) {
+            float cur[kBatch], nxt[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) cur[u] = p[u * s3];
+            for (i3 = kBatch; i3 + kBatch <= n3; i3 += kBatch) {
+#pragma unroll
+              for (int u = 0; u < kBatch; ++u) nxt[u] = p[(i3 + u) * s3];
+#pragma unroll
+              for (int u = 0; u < kBatch; ++u) acc += cur[u];
+#pragma unroll
+              for (int u = 0; u < kBatch; ++u) cur[u] = nxt[u];
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) acc += cur[u];
+          }
+          for (; i3 < n3; ++i3) acc += p[i3 * s3];
         }
     out[t] = acc;
   }

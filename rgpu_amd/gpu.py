@@ -113,6 +113,9 @@ SIGNATURES = {
     "rt_softmax_rows_vjp": (C.c_int, [_VP, _VP, _VP, _VP]),
     "rt_loss": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, _VP]),
     "rt_empty": (C.c_int, [_VP, C.c_int, _SZP, C.c_int, C.POINTER(_VP)]),
+    "rt_adam_many": (C.c_int, [_VP, C.c_int, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP),
+                               C.c_float, C.c_float, C.c_float, C.c_float, C.c_int]),
+    "rt_sgd_many": (C.c_int, [_VP, C.c_int, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP), C.c_float, C.c_float]),
 }
 
 
@@ -337,6 +340,20 @@ class Gpu:
 
     def sgd(self, theta, g, lr: float, momentum: float = 0.0, velocity: Optional[GpuTensor] = None):
         self._call("rt_sgd", self._h, theta.handle, velocity.handle if velocity else None, g.handle, lr, momentum)
+
+    @staticmethod
+    def _handles(ts):
+        return (C.c_void_p * max(len(ts), 1))(*[t.handle if t is not None else None for t in ts])
+
+    def adam_many(self, thetas, ms, vs, gs, lr: float, betas=(0.9, 0.999), t: int = 1, eps: float = 1e-8):
+        """Adam::step over a parameter list (optim.rs:162-198) in one launch per 24 tensors."""
+        self._call("rt_adam_many", self._h, len(thetas), self._handles(thetas), self._handles(ms),
+                   self._handles(vs), self._handles(gs), lr, betas[0], betas[1], eps, t)
+
+    def sgd_many(self, thetas, gs, lr: float, momentum: float = 0.0, velocities=None):
+        """Sgd::step over a parameter list (optim.rs:80-114)."""
+        self._call("rt_sgd_many", self._h, len(thetas), self._handles(thetas),
+                   self._handles(velocities) if velocities is not None else None, self._handles(gs), lr, momentum)
 
     def argmax_rows(self, logits, out):
         """Tensor::argmax_rows (tensor.rs:476-493) into a u32 [B] device buffer."""

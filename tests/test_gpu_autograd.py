@@ -547,3 +547,46 @@ def test_buffer_cache_reuse_keeps_results_correct(gpu):
         want.append(-(x * x))
     for g, w in zip(got, want):
         assert bits_equal(gpu.download(g), w)
+
+
+@pytest.mark.parametrize("kind", ["adam", "sgd", "sgd_momentum"])
+def test_multi_tensor_optimizer_matches_per_tensor(gpu, kind):
+    """rt_adam_many / rt_sgd_many over a list (30 tensors: two launches) are
+    bit-identical to one rt_adam / rt_sgd per tensor."""
+    r = np.random.default_rng(11)
+    shapes = [(int(r.integers(1, 300)), int(r.integers(1, 40))) for _ in range(30)]
+    th = [r.standard_normal(s).astype(np.float32) for s in shapes]
+    gs = [gpu.upload(r.standard_normal(s).astype(np.float32)) for s in shapes]
+    a = [gpu.upload(t) for t in th]
+    b = [gpu.upload(t) for t in th]
+    ma, va = [gpu.zeros(s) for s in shapes], [gpu.zeros(s) for s in shapes]
+    mb, vb = [gpu.zeros(s) for s in shapes], [gpu.zeros(s) for s in shapes]
+    for t in (1, 2, 3):
+        if kind == "adam":
+            gpu.adam_many(a, ma, va, gs, 1e-2, t=t)
+            for i in range(len(shapes)):
+                gpu.adam(b[i], mb[i], vb[i], gs[i], 1e-2, t=t)
+        elif kind == "sgd":
+            gpu.sgd_many(a, gs, 0.1)
+            for i in range(len(shapes)):
+                gpu.sgd(b[i], gs[i], 0.1)
+        else:
+            gpu.sgd_many(a, gs, 0.1, 0.9, ma)
+            for i in range(len(shapes)):
+                gpu.sgd(b[i], gs[i], 0.1, 0.9, mb[i])
+    for x, y in zip(a, b):
+        assert bits_equal(gpu.download(x), gpu.download(y))
+
+
+def test_optimizer_updates_a_repeated_parameter_twice(gpu):
+    """A parameter listed twice is stepped twice, one after the other, as in
+    the reference's loop over params (optim.rs:167-197)."""
+    w = A.Param(gpu, "w", np.array([[1.0, -2.0, 3.0]], np.float32))
+    wo = O.Param(np.array([[1.0, -2.0, 3.0]], np.float32))
+    opt, oo = A.Adam(0.1), O.Optimizer("adam", 0.1)
+    for _ in range(3):
+        opt.step([w, w], w.watch(A.Tape(gpu)).square().sum().backward())
+        t = O.Tape()
+        t.watch(wo).square().sum().backward()
+        oo.step([wo, wo], t)
+    assert bits_equal(w.value(), wo.value())
