@@ -118,7 +118,7 @@ def bench_step(gpu, G, steps, warmup):
     return wall, loss, prof, mlp.dispatches_por_passo()
 
 
-def bench_bwd_gemm(gpu, G, reps=20):
+def bench_bwd_gemm(gpu, G, reps=10, rounds=5):
     """Linear 4096->4096 backward at batch 8192, bf16 operands, f32 accumulate."""
     B, D = 8192, 4096
     rng = np.random.default_rng(3)
@@ -133,15 +133,20 @@ def bench_bwd_gemm(gpu, G, reps=20):
         gpu.gemm(G.NT, gdy, gw, dx)
         gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
     gpu.sync()
-    # Back-to-back launches between two HIP events on the library stream.
-    gpu.timer_begin()
-    for _ in range(reps):
-        gpu.gemm(G.NT, gdy, gw, dx)
-    t_dx = gpu.timer_end() / reps
-    gpu.timer_begin()
-    for _ in range(reps):
-        gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
-    t_dw = gpu.timer_end() / reps
+    # Back-to-back launches between two HIP events on the library stream,
+    # dX and dW alternating in rounds (the sustained clock drifts as the
+    # device warms), median over the rounds.
+    t_dx, t_dw = [], []
+    for _ in range(rounds):
+        gpu.timer_begin()
+        for _ in range(reps):
+            gpu.gemm(G.NT, gdy, gw, dx)
+        t_dx.append(gpu.timer_end() / reps)
+        gpu.timer_begin()
+        for _ in range(reps):
+            gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
+        t_dw.append(gpu.timer_end() / reps)
+    t_dx, t_dw = float(np.median(t_dx)), float(np.median(t_dw))
     flops = 2.0 * B * D * D
     tf_dx = flops / (t_dx * 1e-3) / 1e12
     tf_dw = flops / (t_dw * 1e-3) / 1e12

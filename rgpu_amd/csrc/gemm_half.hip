@@ -63,6 +63,7 @@ struct HalfArgs {
   int mask_bf16;  // mask dtype: 1 = bf16, 0 = f32
   int out_bf16;
   float* colsum;
+  float* cs_parts;  // non-null: per-M-tile column-sum shares [splits * tiles_m, N]
   int k_per_split;
   long long split_stride;
   int tiles_m, tiles_n;
@@ -624,13 +625,16 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
     }
   };
 
-  // Column sums of the (M/N-contiguous) B tiles over k, first M tile only:
-  // thread t sums 8 consecutive columns (chunk t % (BN/8)) over the k rows
-  // t / (BN/8), t / (BN/8) + KG, ... of every stage; the KG partial rows are
-  // added in a fixed order at the end.
+  // Column sums of the (M/N-contiguous) B tiles over k: thread t sums 8
+  // consecutive columns (chunk t % (BN/8)) over the k rows t / (BN/8),
+  // t / (BN/8) + KG, ... of a stage; the KG partial rows are added in a fixed
+  // order at the end.  With cs_parts every M tile takes the stages s with
+  // s % tiles_m == tile_m and writes its share (the shares are added by a
+  // second launch); without it the first M tile sums every stage.
   constexpr int CH = BN / 8, KG = THREADS / CH;
   static_assert(B_KC || (THREADS % CH == 0 && BKD % KG == 0), "colsum split");
-  const bool do_cs = !B_KC && p.colsum != nullptr && tile_m == 0;  // uniform over the block
+  const bool cs_shared = p.cs_parts != nullptr;
+  const bool do_cs = !B_KC && p.colsum != nullptr && (cs_shared || tile_m == 0);  // uniform over the block
   float cs[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   auto colsum = [&](int buf) {
     if constexpr (!B_KC) {
@@ -665,12 +669,20 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
       read_frags(BUF, 1, fa1, fb1);
       mfmas(fa0, fb0);
       interleave(std::integral_constant<int, 0>{});
-      colsum(BUF);
+      if (!cs_shared || k % p.tiles_m == tile_m) colsum(BUF);
       // B: stage k+1 everywhere; stage k no longer read.
       wait_vm<0>();
       barrier_lds();
-      issue(min(k + 2, nk - 1), BUF);
-      read_frags(BUF ^ 1, 0, fa0, fb0);  // (k+1, kk 0); discarded after the last stage
+      // (k+1, kk 0) fragments (discarded after the last stage) and the DMA of
+      // stage k+2 touch different buffers; with a transposed operand the
+      // fragment reads go first (measured faster), else the DMA.
+      if constexpr (A_KC && B_KC) {
+        issue(min(k + 2, nk - 1), BUF);
+        read_frags(BUF ^ 1, 0, fa0, fb0);
+      } else {
+        read_frags(BUF ^ 1, 0, fa0, fb0);
+        issue(min(k + 2, nk - 1), BUF);
+      }
       mfmas(fa1, fb1);
       interleave(std::integral_constant<int, PER_STAGE>{});
     };
@@ -689,14 +701,37 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[kg * BN + 8 * c8 + e] = cs[e];
     __syncthreads();
+    float* dst = cs_shared ? p.cs_parts + ((long long)blockIdx.z * p.tiles_m + tile_m) * p.N
+                           : p.colsum + (long long)blockIdx.z * p.N;
     for (int col = tid; col < BN; col += THREADS) {
       float v = 0.0f;
       for (int j = 0; j < KG; ++j) v += red[j * BN + col];
-      p.colsum[(long long)blockIdx.z * p.N + n0 + col] = v;
+      dst[n0 + col] = v;
     }
   }
 
   store_direct_any<TM, TN>(p, acc, m0, n0, wm, wn, g, r);
+}
+
+// dst[z, n] = sum over t of parts[z * rows + t, n], t in increasing order:
+// the column-sum shares of the M tiles of each K slice z.
+__global__ __launch_bounds__(256) void cs_shares_reduce_kernel(const float* __restrict__ parts, int rows, int splits,
+                                                               int N, float* __restrict__ dst) {
+  const long long i = blockIdx.x * 256LL + threadIdx.x;
+  if (i >= (long long)splits * N) return;
+  const int z = (int)(i / N), n = (int)(i % N);
+  const float* q = parts + (long long)z * rows * N + n;
+  float v = 0.0f;
+  int t = 0;
+  for (; t + 8 <= rows; t += 8) {  // eight loads in flight, added in order
+    float w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) w[u] = q[(long long)(t + u) * N];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v += w[u];
+  }
+  for (; t < rows; ++t) v += q[(long long)t * N];
+  dst[i] = v;
 }
 
 // Direct-to-LDS pipeline shape: K per stage and number of stages.
@@ -728,8 +763,14 @@ bool dma_addressable(const HalfArgs& a) {
 }
 
 template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
-hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16) {
+hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16, float* cs_scratch = nullptr,
+                      size_t cs_scratch_elems = 0) {
   set_tiles<BM, BN>(a);
+  // Column sums shared over the M tiles when there are several and room.
+  a.cs_parts = nullptr;
+  if (!B_KC && a.colsum && a.tiles_m > 1 && cs_scratch &&
+      (size_t)splits * a.tiles_m * a.N <= cs_scratch_elems)
+    a.cs_parts = cs_scratch;
   const dim3 grid(a.tiles_m * a.tiles_n, 1, splits), block(64 * WGM * WGN);
   if (bf16)
     hipLaunchKernelGGL((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true, kDmaBK, kDmaStages>), grid, block, 0,
@@ -737,6 +778,11 @@ hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16) {
   else
     hipLaunchKernelGGL((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false, kDmaBK, kDmaStages>), grid, block,
                        0, s, a);
+  if (a.cs_parts) {
+    const long long n = (long long)splits * a.N;
+    hipLaunchKernelGGL(cs_shares_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.cs_parts,
+                       a.tiles_m, splits, a.N, a.colsum);
+  }
   return hipGetLastError();
 }
 
@@ -751,36 +797,55 @@ hipError_t launch_regs(hipStream_t s, HalfArgs a, int splits, bool bf16) {
   return hipGetLastError();
 }
 
+// Tile size (256, 128 or 64) and kernel (direct-to-LDS or register-staged)
+// for a problem: 256x256 blocks when they give at least one block per CU,
+// 128x128 for mid sizes, 64x64 for small ones.  Full tiles take the
+// direct-to-LDS kernel (256x256: two waves per SIMD with 128x64 wave tiles);
+// the rest the register-staged kernel.
+struct HalfPath {
+  int tile;
+  bool dma;
+};
 template <bool A_KC, bool B_KC>
-hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16) {
-  // 256x256 blocks when they give at least one block per CU, 128x128 for mid
-  // sizes, 64x64 for small ones.  Full tiles take the direct-to-LDS kernel
-  // (256x256: one wave per SIMD with a 128x128 wave tile, the accumulators in
-  // AGPRs); the rest the register-staged kernel (256x256: two waves per SIMD
-  // with 64x128 wave tiles).
+HalfPath pick_path(const HalfArgs& a, int splits) {
   const long long tbig = (long long)((a.M + 255) / 256) * ((a.N + 255) / 256) * splits;
   const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
-  if (tbig >= 256) {
-    if (full_tiles(a, splits, 256, 256) && dma_addressable<A_KC, B_KC>(a))
-      return launch_dma<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
-    return launch_regs<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
+  const int tile = tbig >= 256 ? 256 : t128 >= 128 ? 128 : 64;
+  return HalfPath{tile, full_tiles(a, splits, tile, tile) && dma_addressable<A_KC, B_KC>(a)};
+}
+
+template <bool A_KC, bool B_KC>
+hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* cs_scratch, size_t cs_elems) {
+  const HalfPath hp = pick_path<A_KC, B_KC>(a, splits);
+  switch (hp.tile) {
+    case 256:
+      return hp.dma ? launch_dma<256, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
+                    : launch_regs<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
+    case 128:
+      return hp.dma ? launch_dma<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
+                    : launch_regs<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+    default:
+      return hp.dma ? launch_dma<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
+                    : launch_regs<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
   }
-  if (t128 >= 128) {
-    if (full_tiles(a, splits, 128, 128) && dma_addressable<A_KC, B_KC>(a))
-      return launch_dma<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
-    return launch_regs<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
-  }
-  if (full_tiles(a, splits, 64, 64) && dma_addressable<A_KC, B_KC>(a))
-    return launch_dma<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
-  return launch_regs<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
+}
+
+// Launches launch_half issues: 2 when the column sums are shared over the M
+// tiles (launch_dma's rule), else 1.
+template <bool A_KC, bool B_KC>
+int half_launches(const HalfArgs& a, int splits, size_t cs_elems, bool have_scratch) {
+  if (B_KC || !a.colsum || !have_scratch) return 1;
+  const HalfPath hp = pick_path<A_KC, B_KC>(a, splits);
+  if (!hp.dma) return 1;
+  const int tiles_m = (a.M + hp.tile - 1) / hp.tile;
+  return (tiles_m > 1 && (size_t)splits * tiles_m * a.N <= cs_elems) ? 2 : 1;
 }
 
 }  // namespace
 
 namespace rt {
 
-hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
-  if (d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) return hipErrorInvalidValue;
+static HalfArgs half_args(const GemmDesc& d, int splits) {
   HalfArgs a{};
   a.A = static_cast<const unsigned short*>(d.A);
   a.B = static_cast<const unsigned short*>(d.B);
@@ -795,7 +860,6 @@ hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
   a.bias = d.bias;
   a.mask = d.mask;
   a.mask_bf16 = d.mask_dtype == RT_BF16;
-  const int splits = d.splits < 1 ? 1 : d.splits;
   a.out_bf16 = splits == 1 && d.out_dtype == RT_BF16;
   a.colsum = splits > 1 ? d.colsum_partials : d.colsum;
   int kps = (d.K + splits - 1) / splits;
@@ -805,13 +869,37 @@ hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
   auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   a.vec_a = (d.lda % 8 == 0) && al16(d.A);
   a.vec_b = (d.ldb % 8 == 0) && al16(d.B);
+  return a;
+}
+
+hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
+  if (d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) return hipErrorInvalidValue;
+  const int splits = d.splits < 1 ? 1 : d.splits;
+  const HalfArgs a = half_args(d, splits);
   const bool bf16 = d.in_dtype == RT_BF16;
   switch (d.layout) {
-    case RT_NN: return launch_half<true, false>(s, a, splits, bf16);
-    case RT_TN: return launch_half<false, false>(s, a, splits, bf16);
-    case RT_NT: return launch_half<true, true>(s, a, splits, bf16);
+    case RT_NN: return launch_half<true, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems);
+    case RT_TN: return launch_half<false, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems);
+    case RT_NT: return launch_half<true, true>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems);
   }
   return hipErrorInvalidValue;
+}
+
+int gemm_launch_count(const GemmDesc& d) {
+  if (d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) return 1;
+  const int splits = d.splits < 1 ? 1 : d.splits;
+  const HalfArgs a = half_args(d, splits);
+  const bool have = d.cs_scratch != nullptr;
+  switch (d.layout) {
+    case RT_NN: return half_launches<true, false>(a, splits, d.cs_scratch_elems, have);
+    case RT_TN: return half_launches<false, false>(a, splits, d.cs_scratch_elems, have);
+    default: return 1;
+  }
+}
+
+size_t colsum_scratch_need(int M, int N, int splits) {
+  // The most M tiles any half kernel uses (64-row tiles), per K slice.
+  return (size_t)(splits < 1 ? 1 : splits) * (size_t)((M + 63) / 64) * (size_t)N;
 }
 
 }  // namespace rt

@@ -14,6 +14,7 @@
 //                            the last layer; δ = ∂L/∂Z
 //   partials                 split-K planes (largest user), reused by every
 //                            split GEMM of the step
+//   cs_scratch               column-sum shares of the half dW GEMMs (mixed)
 //   loss_rows [batch]
 //
 // Step (mod.rs:1399-1467 order): forward GEMMs with bias(+ReLU) epilogues;
@@ -71,6 +72,8 @@ struct rt_mlp {
   float* v = nullptr;
   void* theta_h = nullptr;  // bf16 copy
   float* partials = nullptr;
+  float* cs_scratch = nullptr;  // column-sum shares of the half dW GEMMs
+  size_t cs_scratch_elems = 0;
   size_t partial_elems = 0;
   float* loss_rows = nullptr;
   // Mixed precision: [0] applied Adam updates, [1] overflow flag of the last
@@ -107,6 +110,10 @@ static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, co
   d.lda = lda;
   d.ldb = ldb;
   d.ldc = N;
+  if (colsum && in_dtype != RT_F32) {
+    d.cs_scratch = p->cs_scratch;
+    d.cs_scratch_elems = p->cs_scratch_elems;
+  }
   if (splits <= 1) {
     d.C = C;
     d.epi = epi;
@@ -300,6 +307,11 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     }
   }
   p->partial_elems = part;
+  // Column-sum shares of the half dW GEMMs (mixed precision only).
+  size_t cs_elems = 0;
+  if (p->mixed)
+    for (int l = 0; l < n_layers; ++l)
+      cs_elems = std::max(cs_elems, colsum_scratch_need((int)p->L[l].din, (int)p->L[l].dout, p->L[l].splits_dw));
 
   // Arena layout.
   const size_t A = 256;
@@ -324,6 +336,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   std::vector<size_t> o_dw_part(n_layers, 0);
   for (int l = 0; l < n_layers; ++l)
     if (dw_part_elems[l]) o_dw_part[l] = reserve(dw_part_elems[l] * 4);
+  size_t o_cs = cs_elems ? reserve(cs_elems * 4) : 0;
   size_t o_loss = reserve(batch * 4);
   size_t o_state = reserve(16 * 4);
 
@@ -346,6 +359,8 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   p->partials = part ? (float*)(p->arena + o_part) : nullptr;
   for (int l = 0; l < n_layers; ++l) p->L[l].dw_parts = dw_part_elems[l] ? (float*)(p->arena + o_dw_part[l]) : nullptr;
   p->loss_rows = (float*)(p->arena + o_loss);
+  p->cs_scratch = cs_elems ? (float*)(p->arena + o_cs) : nullptr;
+  p->cs_scratch_elems = cs_elems;
   p->state = (int*)(p->arena + o_state);
 
   // Zero everything (padding and moments must start at 0), then upload θ.
@@ -387,6 +402,14 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     const bool fused = l == n_layers - 1 && p->head_fused;
     n += fused ? 1 : (p->L[l].splits_fwd > 1 ? 2 : 1);
     n += (p->L[l].splits_dw > 1 && !p->L[l].dw_parts) ? 2 : 1;
+    if (p->mixed) {  // the dW GEMM may add the shared column sums in a second launch
+      const Layer& Ly = p->L[l];
+      const void* a_in = l == 0 ? nullptr : p->L[l - 1].act;
+      const GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, a_in, Ly.delta_h, p->grad + Ly.w_off, RT_F32, (int)Ly.din,
+                                    (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr,
+                                    RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
+      n += gemm_launch_count(dw) - 1;
+    }
     if (l > 0 && !p->L[l].pair_bwd) n += 1;
   }
   if (!p->head_fused) n += 1;  // softmax-xent

@@ -108,7 +108,16 @@ struct GemmDesc {
   int splits = 1;                 // K slices (blockIdx.z); >1 writes f32 partial planes
   long long split_stride = 0;     // elements between partial planes of C
   float* colsum_partials = nullptr;  // [splits, N] when splits > 1
+  // Optional f32 scratch for the half GEMM's column sums: with room for
+  // colsum_scratch_need(M, N, splits) floats, every M tile of the direct-to-LDS
+  // kernel sums a share of the K stages and a second small launch adds the
+  // shares in a fixed order (otherwise the first M tile sums all of K alone).
+  float* cs_scratch = nullptr;
+  size_t cs_scratch_elems = 0;
 };
+size_t colsum_scratch_need(int M, int N, int splits);
+// Kernel launches gemm_launch issues for d (1, or 2 with shared column sums).
+int gemm_launch_count(const GemmDesc& d);
 
 // Enqueues C (or its partial planes) on stream.  Shapes and pointers are
 // validated by the caller.

@@ -457,6 +457,11 @@ int rt_gemm(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_bu
     d.mask_dtype = aux->dtype;
   }
   d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
+  if (colsum && is_half(a->dtype)) {
+    if ((rc = ensure_scratch(c, colsum_scratch_need(d.M, d.N, 1)))) return rc;
+    d.cs_scratch = c->scratch;
+    d.cs_scratch_elems = c->scratch_elems;
+  }
   Launch L(c, layout == RT_NN ? "gemm_nn" : layout == RT_TN ? "gemm_tn" : "gemm_nt");
   HIP_TRY(c, gemm_launch(c->stream, d), "gemm launch");
   return RT_OK;
@@ -505,6 +510,11 @@ int rt_gemm_splitk(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b
   d.ldb = (int)b->shape[1];
   d.ldc = (int)N;
   float* part = static_cast<float*>(partials->ptr);
+  if (colsum && is_half(a->dtype)) {
+    if ((rc = ensure_scratch(c, colsum_scratch_need(d.M, d.N, (int)slices)))) return rc;
+    d.cs_scratch = c->scratch;
+    d.cs_scratch_elems = c->scratch_elems;
+  }
   if (slices == 1) {
     d.C = out->ptr;
     d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
