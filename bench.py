@@ -1,6 +1,6 @@
 """Benchmark of the MLP training step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only all|step|bwd|splitk|mixed|tape]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only all|step|bwd|splitk|mixed|tape|pcie]
 
 Workload (one "step"): MLP 512->1024(ReLU)->1024(ReLU)->10, f32, batch 2048,
 softmax cross-entropy, Adam(1e-3, 0.9, 0.999, 1e-8): forward, backward and the
@@ -17,6 +17,8 @@ better).  Next to it:
                 the HBM roofline
   mixed_mlp     8 x 4096 ReLU MLP -> 1000 classes, batch 4096, bf16 with f32
                 master weights, loss scale 1024, Adam: ms/step and TFLOP/s
+  pcie_inclusive  the same step with every batch copied from host memory:
+                synchronous writes vs. the overlapped loader (not `value`)
   tape_mlp      examples/bench_grande.rs (N 4096, D 128, H 512, minibatch
                 256, Adam) trained through the device autodiff tape, one
                 HIP launch per recorded op, against the oracle's CPU tape
@@ -327,6 +329,46 @@ def cpu_tape_baseline(budget_s=10.0):
             "sample": f"{n} minibatch steps of bench_grande (lote {TAPE_LOTE}) on the oracle tape, 1 thread"}
 
 
+def bench_pcie(gpu, G, steps=50):
+    """The batch-2048 f32 step with each batch coming from host memory
+    (PCIe-inclusive; `value` never includes this): (a) rt_write of x and the
+    labels into the batch buffers, then the step (the write waits for the
+    previous step); (b) rt_mlp_load + rt_mlp_step_loaded, the copy of batch
+    i+1 overlapping step i."""
+    rng = np.random.default_rng(11)
+    params = []
+    for l in range(len(DIMS) - 1):
+        params += [kaiming(rng, DIMS[l], DIMS[l + 1]), np.zeros((1, DIMS[l + 1]), np.float32)]
+    xs = [rng.standard_normal((BATCH, DIMS[0]), dtype=np.float32) for _ in range(4)]
+    ys = [rng.integers(0, DIMS[-1], BATCH) for _ in range(4)]
+    ys32 = [y.astype(np.uint32) for y in ys]
+    out = {}
+    for mode in ("write_then_step", "overlapped_load"):
+        mlp = G.GpuMlp.from_params(gpu, params, BATCH, 1e-3)
+        xb, yb = gpu.zeros((BATCH, DIMS[0])), gpu.zeros((BATCH,), G.U32)
+
+        def one(i):
+            if mode == "write_then_step":
+                gpu.write(xb, xs[i % 4])
+                gpu.write(yb, ys32[i % 4])
+                mlp.step(xb, yb)
+            else:
+                mlp.carregar(xs[i % 4], ys[i % 4])
+                mlp.step_loaded()
+
+        for i in range(5):
+            one(i)
+        gpu.sync()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            one(i)
+        gpu.sync()
+        out[mode + "_ms"] = round((time.perf_counter() - t0) / steps * 1e3, 4)
+        mlp.destroy()
+    out["batch_bytes"] = BATCH * DIMS[0] * 4 + BATCH * 4
+    return out
+
+
 def bench_copy(gpu, G, mib=256, reps=5):
     """A plain device copy of known size (f32 -> f32 through the convert
     kernel): reads and writes exactly mib MiB per launch.  Used to calibrate
@@ -380,7 +422,7 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy", "tape"], default="all",
+    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy", "tape", "pcie"], default="all",
                     help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -391,9 +433,9 @@ def main():
     from rgpu_amd import gpu as G
 
     gpu = G.Gpu(0)
-    if args.only in ("bwd", "splitk", "mixed", "copy", "tape"):
+    if args.only in ("bwd", "splitk", "mixed", "copy", "tape", "pcie"):
         fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed, "copy": bench_copy,
-              "tape": bench_tape}[args.only]
+              "tape": bench_tape, "pcie": bench_pcie}[args.only]
         print(json.dumps({args.only: fn(gpu, G)}), flush=True)
         return
     wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
@@ -447,6 +489,7 @@ def main():
         out["splitk_dw"] = bench_splitk(gpu, G)
         out["mixed_mlp"] = bench_mixed(gpu, G)
         out["tape_mlp"] = bench_tape(gpu, G)
+        out["pcie_inclusive"] = bench_pcie(gpu, G)
     if not args.no_cpu:
         cb = cpu_baseline()
         out["cpu_baseline"] = cb

@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -76,6 +77,18 @@ struct rt_mlp {
   size_t cs_scratch_elems = 0;
   size_t partial_elems = 0;
   float* loss_rows = nullptr;
+  // Double-buffered batch slots for rt_mlp_load / rt_mlp_step_loaded: pinned
+  // host staging, device copies, and per slot the event of its last
+  // host-to-device copy (copy stream) and of the last step that read it.
+  struct Slot {
+    void* x_host = nullptr;
+    uint32_t* y_host = nullptr;
+    rt_buf x, y;
+    hipEvent_t copied = nullptr, used = nullptr;
+    bool copy_pending = false, use_pending = false;
+  } slot[2];
+  bool slots_ready = false;
+  int next_slot = 0, loaded = -1;
   // Mixed precision: [0] applied Adam updates, [1] overflow flag of the last
   // step, [2] a step was issued (see step_begin_launch).
   int* state = nullptr;
@@ -241,8 +254,49 @@ static int opt_launches(const rt_mlp* p) {
 namespace rt {
 void mlp_release(rt_mlp* p) {
   hipStreamSynchronize(p->ctx->stream);
+  if (p->ctx->copy_stream) hipStreamSynchronize(p->ctx->copy_stream);
+  for (auto& s : p->slot) {
+    if (s.x_host) hipHostFree(s.x_host);
+    if (s.y_host) hipHostFree(s.y_host);
+    if (s.x.ptr) hipFree(s.x.ptr);
+    if (s.y.ptr) hipFree(s.y.ptr);
+    if (s.copied) hipEventDestroy(s.copied);
+    if (s.used) hipEventDestroy(s.used);
+  }
   hipFree(p->arena);
   delete p;
+}
+
+// Allocates the two batch slots on first use.
+static int ensure_slots(rt_mlp* p) {
+  if (p->slots_ready) return RT_OK;
+  rt_ctx* c = p->ctx;
+  hipError_t e = hipSuccess;
+  if (!c->copy_stream) e = hipStreamCreateWithFlags(&c->copy_stream, hipStreamNonBlocking);
+  const rt_dtype xd = p->mixed ? RT_BF16 : RT_F32;
+  const size_t xn = p->batch * p->L[0].din, xb = xn * dtype_size(xd), yb = p->batch * 4;
+  for (auto& s : p->slot) {
+    if (e == hipSuccess) e = hipHostMalloc(&s.x_host, xb, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&s.y_host, yb, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(&s.x.ptr, (xb + 255) / 256 * 256);
+    if (e == hipSuccess) e = hipMalloc(&s.y.ptr, (yb + 255) / 256 * 256);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.copied, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.used, hipEventDisableTiming);
+    s.x.dtype = xd;
+    s.x.rank = 2;
+    s.x.shape[0] = p->batch;
+    s.x.shape[1] = p->L[0].din;
+    s.x.n = xn;
+    s.x.bytes = xb;
+    s.y.dtype = RT_U32;
+    s.y.rank = 1;
+    s.y.shape[0] = p->batch;
+    s.y.n = p->batch;
+    s.y.bytes = yb;
+  }
+  if (e != hipSuccess) return hip_fail(c, e, "batch slots");  // freed with the plan
+  p->slots_ready = true;
+  return RT_OK;
 }
 }  // namespace rt
 
@@ -542,6 +596,47 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     hipError_t e = optimizer_launch(c->stream, ts.data() + i0, nt, P);
     if (e != hipSuccess) return hip_fail(c, e, "optimizer");
   }
+  return RT_OK;
+}
+
+int rt_mlp_load(rt_mlp* p, const void* x, size_t x_bytes, const uint64_t* labels, size_t n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  if (x == nullptr || labels == nullptr) return fail(c, RT_ERR_INVALID, "null batch");
+  int rc = ensure_slots(p);
+  if (rc) return rc;
+  const int k = p->next_slot;
+  auto& s = p->slot[k];
+  if (x_bytes != s.x.bytes) return fail(c, RT_ERR_SHAPE, "batch of %zu bytes, plan takes %zu", x_bytes, s.x.bytes);
+  if (n != p->batch) return fail(c, RT_ERR_SHAPE, "%zu labels, plan takes %zu", n, p->batch);
+  for (size_t i = 0; i < n; ++i)
+    if (labels[i] > 0xffffffffULL) return fail(c, RT_ERR_LABEL, "label %zu does not fit u32", i);
+  // The staging buffers are free once this slot's previous copy has run.
+  if (s.copy_pending) HIP_TRY(c, hipEventSynchronize(s.copied), "staging wait");
+  std::memcpy(s.x_host, x, x_bytes);
+  for (size_t i = 0; i < n; ++i) s.y_host[i] = (uint32_t)labels[i];
+  // The device slot is free once the last step that read it has run; steps
+  // on the other slot run meanwhile (the overlap).
+  if (s.use_pending) HIP_TRY(c, hipStreamWaitEvent(c->copy_stream, s.used, 0), "slot wait");
+  HIP_TRY(c, hipMemcpyAsync(s.x.ptr, s.x_host, s.x.bytes, hipMemcpyHostToDevice, c->copy_stream), "batch copy");
+  HIP_TRY(c, hipMemcpyAsync(s.y.ptr, s.y_host, s.y.bytes, hipMemcpyHostToDevice, c->copy_stream), "label copy");
+  HIP_TRY(c, hipEventRecord(s.copied, c->copy_stream), "copy event");
+  s.copy_pending = true;
+  p->loaded = k;
+  p->next_slot = k ^ 1;
+  return RT_OK;
+}
+
+int rt_mlp_step_loaded(rt_mlp* p) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  rt_ctx* c = p->ctx;
+  if (p->loaded < 0) return fail(c, RT_ERR_INVALID, "no batch loaded");
+  auto& s = p->slot[p->loaded];
+  HIP_TRY(c, hipStreamWaitEvent(c->stream, s.copied, 0), "copy wait");
+  int rc = rt_mlp_step(p, &s.x, &s.y);
+  if (rc) return rc;
+  HIP_TRY(c, hipEventRecord(s.used, c->stream), "use event");
+  s.use_pending = true;
   return RT_OK;
 }
 

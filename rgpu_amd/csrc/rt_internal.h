@@ -53,6 +53,9 @@ struct rt_ctx {
   // Region timer (rt_timer_begin / rt_timer_end).
   hipEvent_t timer0 = nullptr, timer1 = nullptr;
   bool timer_running = false;
+  // Host-to-device copies of staged batches (rt_mlp_load), created on first
+  // use; default priority like the main stream.
+  hipStream_t copy_stream = nullptr;
 };
 
 namespace rt {

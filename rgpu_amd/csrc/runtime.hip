@@ -169,6 +169,7 @@ int rt_close(rt_ctx* c) {
   if (c->timer1) hipEventDestroy(c->timer1);
   hipFree(c->d_flags);
   if (c->scratch) hipFree(c->scratch);
+  if (c->copy_stream) hipStreamDestroy(c->copy_stream);
   hipStreamDestroy(c->stream);
   delete c;
   return RT_OK;

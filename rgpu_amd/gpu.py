@@ -115,6 +115,8 @@ SIGNATURES = {
     "rt_empty": (C.c_int, [_VP, C.c_int, _SZP, C.c_int, C.POINTER(_VP)]),
     "rt_adam_many": (C.c_int, [_VP, C.c_int, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP),
                                C.c_float, C.c_float, C.c_float, C.c_float, C.c_int]),
+    "rt_mlp_load": (C.c_int, [_VP, _VP, C.c_size_t, C.POINTER(C.c_uint64), C.c_size_t]),
+    "rt_mlp_step_loaded": (C.c_int, [_VP]),
     "rt_sgd_many": (C.c_int, [_VP, C.c_int, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP), C.c_float, C.c_float]),
 }
 
@@ -448,11 +450,12 @@ class GpuMlp:
     """``GpuMlp`` (mod.rs:1322-1562): ReLU hidden layers, linear output,
     softmax cross-entropy, trained entirely on the device."""
 
-    def __init__(self, gpu: Gpu, handle: int, dims: Sequence[int], batch: int):
+    def __init__(self, gpu: Gpu, handle: int, dims: Sequence[int], batch: int, precision: str = "f32"):
         self.gpu = gpu
         self._h = handle
         self.dims = list(dims)
         self.lote = batch
+        self.precision = precision
 
     @classmethod
     def from_params(cls, gpu: Gpu, params: Sequence[np.ndarray], lote: int, lr: float, optimizer: str = "adam",
@@ -472,7 +475,7 @@ class GpuMlp:
         d = (C.c_size_t * (n + 1))(*dims)
         h = C.c_void_p()
         gpu._call("rt_mlp_create", gpu._h, n, d, wp, bp, lote, C.byref(cfg), C.byref(h))
-        return cls(gpu, h.value, dims, lote)
+        return cls(gpu, h.value, dims, lote, precision)
 
     def destroy(self):
         # A closed Gpu already released its models.
@@ -488,6 +491,26 @@ class GpuMlp:
 
     def step(self, x: GpuTensor, labels: GpuTensor) -> None:
         self.gpu._call("rt_mlp_step", self._h, x.handle, labels.handle)
+
+    def carregar(self, x, labels) -> None:
+        """GpuMlp::carregar (mod.rs:1486-1495), overlapped: stage a host batch
+        (f32, or bf16 bits / f32 values for a bf16 plan) and its labels; the
+        host-to-device copy runs while earlier steps compute."""
+        x = np.asarray(x)
+        if self.precision == "bf16":
+            host = x if x.dtype == np.uint16 else f32_to_bf16_bits(x)
+        else:
+            host = x.astype(np.float32, copy=False)
+        host = np.ascontiguousarray(host)
+        lab = np.ascontiguousarray(np.asarray(labels).astype(np.uint64))
+        self.gpu._call("rt_mlp_load", self._h, host.ctypes.data_as(C.c_void_p), host.nbytes,
+                       lab.ctypes.data_as(C.POINTER(C.c_uint64)), lab.size)
+
+    load = carregar
+
+    def step_loaded(self) -> None:
+        """rt_mlp_step on the most recently loaded batch."""
+        self.gpu._call("rt_mlp_step_loaded", self._h)
 
     def forward_only(self, x: GpuTensor) -> None:
         self.gpu._call("rt_mlp_forward", self._h, x.handle)
