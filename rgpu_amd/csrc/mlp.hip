@@ -294,7 +294,18 @@ static int ensure_slots(rt_mlp* p) {
     s.y.n = p->batch;
     s.y.bytes = yb;
   }
-  if (e != hipSuccess) return hip_fail(c, e, "batch slots");  // freed with the plan
+  if (e != hipSuccess) {  // undo the partial allocation; a later call may retry
+    for (auto& sl : p->slot) {
+      if (sl.x_host) hipHostFree(sl.x_host);
+      if (sl.y_host) hipHostFree(sl.y_host);
+      if (sl.x.ptr) hipFree(sl.x.ptr);
+      if (sl.y.ptr) hipFree(sl.y.ptr);
+      if (sl.copied) hipEventDestroy(sl.copied);
+      if (sl.used) hipEventDestroy(sl.used);
+      sl = rt_mlp::Slot();
+    }
+    return hip_fail(c, e, "batch slots");
+  }
   p->slots_ready = true;
   return RT_OK;
 }
