@@ -68,6 +68,7 @@ struct HalfArgs {
   long long split_stride;
   int tiles_m, tiles_n;
   int vec_a, vec_b;
+  int n_ragged;  // N is not a multiple of BN: B tiles read past column N, stores and sums stop at N
 };
 
 __device__ inline float bf16_to_f32(unsigned short h) { return __uint_as_float((unsigned int)h << 16); }
@@ -467,6 +468,7 @@ __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[
 #pragma unroll
     for (int u = 0; u < TN; ++u) {
       const int col = n0 + wn + 16 * u + 4 * g;
+      if (p.n_ragged && col >= p.N) continue;  // N % 4 == 0: a group is all in or all out
       const long long off = row_off + col;
       f4 v = acc[t][u];
       if constexpr (EPI == RT_EPI_BIAS || EPI == RT_EPI_BIAS_RELU) {
@@ -703,7 +705,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
     __syncthreads();
     float* dst = cs_shared ? p.cs_parts + ((long long)blockIdx.z * p.tiles_m + tile_m) * p.N
                            : p.colsum + (long long)blockIdx.z * p.N;
-    for (int col = tid; col < BN; col += THREADS) {
+    for (int col = tid; col < BN && n0 + col < p.N; col += THREADS) {
       float v = 0.0f;
       for (int j = 0; j < KG; ++j) v += red[j * BN + col];
       dst[n0 + col] = v;
@@ -745,13 +747,16 @@ void set_tiles(HalfArgs& a) {
 
 // Whole BM x BN tiles everywhere, every K slice (the last included) a
 // multiple of the DMA stage, and operands the DMA can read 16 bytes at a time.
-bool full_tiles(const HalfArgs& a, int splits, int BM, int BN) {
+// With n_ragged_ok, N need only be a multiple of 8 (the caller guarantees
+// that B may be read up to BN columns past its last element).
+bool full_tiles(const HalfArgs& a, int splits, int BM, int BN, bool n_ragged_ok = false) {
   const int last = a.K - (splits - 1) * a.k_per_split;
   auto al = [](const void* ptr, unsigned n) { return (reinterpret_cast<uintptr_t>(ptr) & (n - 1)) == 0; };
   const bool bf16_out = splits == 1 && a.out_bf16;
   const bool epi_ok = (a.epi != RT_EPI_BIAS && a.epi != RT_EPI_BIAS_RELU) || al(a.bias, 16);
   const bool mask_ok = a.epi != RT_EPI_RELU_MASK || al(a.mask, a.mask_bf16 ? 8 : 16);
-  return a.M % BM == 0 && a.N % BN == 0 && a.k_per_split % kDmaBK == 0 && last > 0 && last % kDmaBK == 0 &&
+  const bool n_ok = a.N % BN == 0 || (n_ragged_ok && a.N % 8 == 0);
+  return a.M % BM == 0 && n_ok && a.k_per_split % kDmaBK == 0 && last > 0 && last % kDmaBK == 0 &&
          a.vec_a && a.vec_b && a.ldc % 4 == 0 && al(a.C, bf16_out ? 8 : 16) && epi_ok && mask_ok;
 }
 
@@ -807,16 +812,19 @@ struct HalfPath {
   bool dma;
 };
 template <bool A_KC, bool B_KC>
-HalfPath pick_path(const HalfArgs& a, int splits) {
+HalfPath pick_path(const HalfArgs& a, int splits, bool overread_ok) {
   const long long tbig = (long long)((a.M + 255) / 256) * ((a.N + 255) / 256) * splits;
   const long long t128 = (long long)((a.M + 127) / 128) * ((a.N + 127) / 128) * splits;
   const int tile = tbig >= 256 ? 256 : t128 >= 128 ? 128 : 64;
-  return HalfPath{tile, full_tiles(a, splits, tile, tile) && dma_addressable<A_KC, B_KC>(a)};
+  // A ragged N is read past its end only along B's rows (N-contiguous B).
+  return HalfPath{tile, full_tiles(a, splits, tile, tile, overread_ok && !B_KC) && dma_addressable<A_KC, B_KC>(a)};
 }
 
 template <bool A_KC, bool B_KC>
-hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* cs_scratch, size_t cs_elems) {
-  const HalfPath hp = pick_path<A_KC, B_KC>(a, splits);
+hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* cs_scratch, size_t cs_elems,
+                       bool overread_ok) {
+  const HalfPath hp = pick_path<A_KC, B_KC>(a, splits, overread_ok);
+  a.n_ragged = hp.dma && a.N % hp.tile != 0;
   switch (hp.tile) {
     case 256:
       return hp.dma ? launch_dma<256, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
@@ -833,9 +841,9 @@ hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* 
 // Launches launch_half issues: 2 when the column sums are shared over the M
 // tiles (launch_dma's rule), else 1.
 template <bool A_KC, bool B_KC>
-int half_launches(const HalfArgs& a, int splits, size_t cs_elems, bool have_scratch) {
+int half_launches(const HalfArgs& a, int splits, size_t cs_elems, bool have_scratch, bool overread_ok) {
   if (B_KC || !a.colsum || !have_scratch) return 1;
-  const HalfPath hp = pick_path<A_KC, B_KC>(a, splits);
+  const HalfPath hp = pick_path<A_KC, B_KC>(a, splits, overread_ok);
   if (!hp.dma) return 1;
   const int tiles_m = (a.M + hp.tile - 1) / hp.tile;
   return (tiles_m > 1 && (size_t)splits * tiles_m * a.N <= cs_elems) ? 2 : 1;
@@ -878,9 +886,9 @@ hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
   const HalfArgs a = half_args(d, splits);
   const bool bf16 = d.in_dtype == RT_BF16;
   switch (d.layout) {
-    case RT_NN: return launch_half<true, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems);
-    case RT_TN: return launch_half<false, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems);
-    case RT_NT: return launch_half<true, true>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems);
+    case RT_NN: return launch_half<true, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
+    case RT_TN: return launch_half<false, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
+    case RT_NT: return launch_half<true, true>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
   }
   return hipErrorInvalidValue;
 }
@@ -891,8 +899,8 @@ int gemm_launch_count(const GemmDesc& d) {
   const HalfArgs a = half_args(d, splits);
   const bool have = d.cs_scratch != nullptr;
   switch (d.layout) {
-    case RT_NN: return half_launches<true, false>(a, splits, d.cs_scratch_elems, have);
-    case RT_TN: return half_launches<false, false>(a, splits, d.cs_scratch_elems, have);
+    case RT_NN: return half_launches<true, false>(a, splits, d.cs_scratch_elems, have, d.overread_ok);
+    case RT_TN: return half_launches<false, false>(a, splits, d.cs_scratch_elems, have, d.overread_ok);
     default: return 1;
   }
 }

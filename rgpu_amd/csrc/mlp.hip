@@ -112,6 +112,7 @@ static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, co
                           int M, int N, int K, int lda, int ldb, int epi, const float* bias, const void* mask,
                           int mask_dtype, float* colsum, int splits, float* parts = nullptr) {
   GemmDesc d;
+  d.overread_ok = true;  // every arena region is followed by >= 1 KiB of slack; x is never a B operand
   d.layout = layout;
   d.in_dtype = in_dtype;
   d.out_dtype = out_dtype;
@@ -381,9 +382,11 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   // Arena layout.
   const size_t A = 256;
   size_t bytes = 0;
+  // Each region is followed by 1 KiB of slack, so a GEMM may over-read the
+  // last row of a B operand whose width is not a multiple of its tile.
   auto reserve = [&](size_t nbytes) {
     size_t o = bytes;
-    bytes += round_up(std::max<size_t>(nbytes, 1), A);
+    bytes += round_up(std::max<size_t>(nbytes, 1), A) + 1024;
     return o;
   };
   size_t o_theta = reserve(p->n_params * 4), o_grad = reserve(p->n_params * 4), o_m = reserve(p->n_params * 4),

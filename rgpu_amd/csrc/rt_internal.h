@@ -117,6 +117,10 @@ struct GemmDesc {
   // shares in a fixed order (otherwise the first M tile sums all of K alone).
   float* cs_scratch = nullptr;
   size_t cs_scratch_elems = 0;
+  // The caller guarantees that A and B may be read up to 1 KiB past their
+  // last element (memory inside the same allocation): lets the half GEMM's
+  // direct-to-LDS kernel take an N that is not a multiple of its tile.
+  bool overread_ok = false;
 };
 size_t colsum_scratch_need(int M, int N, int splits);
 // Kernel launches gemm_launch issues for d (1, or 2 with shared column sums).
