@@ -69,7 +69,10 @@ struct HalfArgs {
   int tiles_m, tiles_n;
   int vec_a, vec_b;
   int n_ragged;  // N is not a multiple of BN: B tiles read past column N, stores and sums stop at N
+  int* nf_flag;  // non-null: set to 1 if any f32 result (C or column sums) is not finite
 };
+
+__device__ inline int not_finite(float v) { return !(fabsf(v) <= 3.402823466e38f); }
 
 __device__ inline float bf16_to_f32(unsigned short h) { return __uint_as_float((unsigned int)h << 16); }
 
@@ -462,6 +465,7 @@ __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[
                                              int wn, int g, int r) {
   float* Cf = static_cast<float*>(p.C) + (gridDim.z > 1 ? (long long)blockIdx.z * p.split_stride : 0);
   unsigned short* Ch = static_cast<unsigned short*>(p.C);
+  int bad = 0;
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
     const long long row_off = (long long)(m0 + wm + 16 * t + r) * p.ldc;
@@ -498,9 +502,11 @@ __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[
         *reinterpret_cast<u2*>(Ch + off) = w;
       } else {
         *reinterpret_cast<f4*>(Cf + off) = v;
+        bad |= not_finite(v[0]) | not_finite(v[1]) | not_finite(v[2]) | not_finite(v[3]);
       }
     }
   }
+  if (bad && p.nf_flag) *p.nf_flag = 1;
 }
 
 template <int TM, int TN>
@@ -705,11 +711,14 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
     __syncthreads();
     float* dst = cs_shared ? p.cs_parts + ((long long)blockIdx.z * p.tiles_m + tile_m) * p.N
                            : p.colsum + (long long)blockIdx.z * p.N;
+    int bad = 0;
     for (int col = tid; col < BN && n0 + col < p.N; col += THREADS) {
       float v = 0.0f;
       for (int j = 0; j < KG; ++j) v += red[j * BN + col];
       dst[n0 + col] = v;
+      bad |= not_finite(v);
     }
+    if (bad && p.nf_flag && !cs_shared) *p.nf_flag = 1;  // shares are checked once summed
   }
 
   store_direct_any<TM, TN>(p, acc, m0, n0, wm, wn, g, r);
@@ -718,7 +727,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
 // dst[z, n] = sum over t of parts[z * rows + t, n], t in increasing order:
 // the column-sum shares of the M tiles of each K slice z.
 __global__ __launch_bounds__(256) void cs_shares_reduce_kernel(const float* __restrict__ parts, int rows, int splits,
-                                                               int N, float* __restrict__ dst) {
+                                                               int N, float* __restrict__ dst, int* nf_flag) {
   const long long i = blockIdx.x * 256LL + threadIdx.x;
   if (i >= (long long)splits * N) return;
   const int z = (int)(i / N), n = (int)(i % N);
@@ -734,6 +743,7 @@ __global__ __launch_bounds__(256) void cs_shares_reduce_kernel(const float* __re
   }
   for (; t < rows; ++t) v += q[(long long)t * N];
   dst[i] = v;
+  if (nf_flag && not_finite(v)) *nf_flag = 1;
 }
 
 // Direct-to-LDS pipeline shape: K per stage and number of stages.
@@ -786,7 +796,7 @@ hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16, float* c
   if (a.cs_parts) {
     const long long n = (long long)splits * a.N;
     hipLaunchKernelGGL(cs_shares_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.cs_parts,
-                       a.tiles_m, splits, a.N, a.colsum);
+                       a.tiles_m, splits, a.N, a.colsum, a.nf_flag);
   }
   return hipGetLastError();
 }
@@ -825,6 +835,7 @@ hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* 
                        bool overread_ok) {
   const HalfPath hp = pick_path<A_KC, B_KC>(a, splits, overread_ok);
   a.n_ragged = hp.dma && a.N % hp.tile != 0;
+  if (!hp.dma || splits > 1) a.nf_flag = nullptr;  // gemm_checks_nonfinite says false for these
   switch (hp.tile) {
     case 256:
       return hp.dma ? launch_dma<256, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
@@ -877,6 +888,7 @@ static HalfArgs half_args(const GemmDesc& d, int splits) {
   auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
   a.vec_a = (d.lda % 8 == 0) && al16(d.A);
   a.vec_b = (d.ldb % 8 == 0) && al16(d.B);
+  a.nf_flag = d.nf_flag;
   return a;
 }
 
@@ -891,6 +903,17 @@ hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
     case RT_NT: return launch_half<true, true>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
   }
   return hipErrorInvalidValue;
+}
+
+bool gemm_checks_nonfinite(const GemmDesc& d) {
+  if (d.nf_flag == nullptr || (d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) || d.splits > 1) return false;
+  const HalfArgs a = half_args(d, 1);
+  switch (d.layout) {
+    case RT_NN: return pick_path<true, false>(a, 1, d.overread_ok).dma;
+    case RT_TN: return pick_path<false, false>(a, 1, d.overread_ok).dma;
+    case RT_NT: return pick_path<true, true>(a, 1, d.overread_ok).dma;
+  }
+  return false;
 }
 
 int gemm_launch_count(const GemmDesc& d) {

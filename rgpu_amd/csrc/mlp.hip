@@ -482,7 +482,19 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   }
   if (!p->head_fused) n += 1;  // softmax-xent
   n += opt_launches(p);  // optimizer
-  if (p->mixed) n += 2;  // step prologue + non-finite check
+  if (p->mixed) {
+    n += 1;  // step prologue
+    int unchecked = 0;  // layers whose dW GEMM cannot flag non-finite values itself
+    for (int l = 0; l < n_layers; ++l) {
+      const Layer& Ly = p->L[l];
+      GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, l == 0 ? nullptr : p->L[l - 1].act, Ly.delta_h, p->grad + Ly.w_off,
+                              RT_F32, (int)Ly.din, (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE,
+                              nullptr, nullptr, RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
+      dw.nf_flag = p->state + 1;
+      unchecked += !gemm_checks_nonfinite(dw);
+    }
+    n += (2 * unchecked + kMaxOptTensors - 1) / kMaxOptTensors;  // separate checks, 24 tensors per launch
+  }
   p->dispatches = n;
   c->mlps.push_back(p);
   *out = p;
@@ -527,14 +539,22 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   if ((rc = run_forward(p, x, labels, scale))) return rc;
 
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
+  std::vector<char> unchecked(nl, 1);
   for (int l = nl - 1; l >= 0; --l) {
     Layer& Ly = p->L[l];
     const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
     const void* dl = p->mixed ? Ly.delta_h : (const void*)Ly.delta;
     // dW_l = A_{l-1}ᵀ·δ_l  (TN; A stored [batch, din]), db_l = 1ᵀ·δ_l fused.
-    const GemmDesc dw = plan_desc(p, RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32, (int)Ly.din, (int)Ly.dout,
-                                  B, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32,
-                                  p->grad + Ly.b_off, Ly.splits_dw, Ly.dw_parts);
+    GemmDesc dw = plan_desc(p, RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32, (int)Ly.din, (int)Ly.dout, B,
+                            (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32, p->grad + Ly.b_off,
+                            Ly.splits_dw, Ly.dw_parts);
+    if (p->mixed) {
+      // The overflow flag is set by the GEMM's own epilogue where it can;
+      // the other layers' dW/db go to the separate check below.
+      dw.nf_flag = overflow;
+      unchecked[l] = !gemm_checks_nonfinite(dw);
+      if (unchecked[l]) dw.nf_flag = nullptr;
+    }
     if (l == 0) {
       {
         Launch Lz(c, Ly.lbl_dw.c_str());
@@ -573,11 +593,21 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   }
 
   if (p->mixed) {
-    const float* ptrs[1] = {p->grad};
-    size_t ns[1] = {p->n_params};
-    Launch Lz(c, "nonfinite_check");
-    hipError_t e = nonfinite_check_launch(c->stream, ptrs, ns, 1, overflow);
-    if (e != hipSuccess) return hip_fail(c, e, "non-finite check");
+    std::vector<const float*> ptrs;
+    std::vector<size_t> ns;
+    for (int l = 0; l < nl; ++l) {
+      if (!unchecked[l]) continue;
+      ptrs.push_back(p->grad + p->L[l].w_off);
+      ns.push_back(p->L[l].din * p->L[l].dout);
+      ptrs.push_back(p->grad + p->L[l].b_off);
+      ns.push_back(p->L[l].dout);
+    }
+    for (size_t i = 0; i < ptrs.size(); i += kMaxOptTensors) {
+      const int k = (int)std::min<size_t>(kMaxOptTensors, ptrs.size() - i);
+      Launch Lz(c, "nonfinite_check");
+      hipError_t e = nonfinite_check_launch(c->stream, ptrs.data() + i, ns.data() + i, k, overflow);
+      if (e != hipSuccess) return hip_fail(c, e, "non-finite check");
+    }
   }
 
   p->t += 1;

@@ -121,7 +121,11 @@ struct GemmDesc {
   // last element (memory inside the same allocation): lets the half GEMM's
   // direct-to-LDS kernel take an N that is not a multiple of its tile.
   bool overread_ok = false;
+  // Optional: set *nf_flag = 1 if any f32 result is not finite.  Honoured
+  // only where gemm_checks_nonfinite(d) is true.
+  int* nf_flag = nullptr;
 };
+bool gemm_checks_nonfinite(const GemmDesc& d);
 size_t colsum_scratch_need(int M, int N, int splits);
 // Kernel launches gemm_launch issues for d (1, or 2 with shared column sums).
 int gemm_launch_count(const GemmDesc& d);

@@ -132,19 +132,23 @@ def test_mixed_precision_mlp_full_size_steps(gpu):
     assert max(d) < 2e-2
 
 
-def test_mixed_precision_overflow_skips_update(gpu):
+@pytest.mark.parametrize("dims,batch", [
+    ([64, 64, 10], 32),      # register-staged GEMMs: the separate non-finite check
+    ([128, 256, 128], 128),  # direct-to-LDS dW GEMMs: the flag comes from their epilogues alone
+    ([128, 256, 100], 128),  # both: the 100-wide head is checked separately
+])
+def test_mixed_precision_overflow_skips_update(gpu, dims, batch):
     # A huge input makes the scaled gradient overflow: the step is skipped
     # (weights unchanged) and reported, and training continues afterwards.
-    dims = [64, 64, 10]
     params = kaiming_model(8, dims)
-    mlp = G.GpuMlp.from_params(gpu, params, 32, 1e-3, precision="bf16", loss_scale=1024.0)
+    mlp = G.GpuMlp.from_params(gpu, params, batch, 1e-3, precision="bf16", loss_scale=1024.0)
     w0 = mlp.weights()
-    x = np.full((32, 64), 3.0e38, np.float32)
-    mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, np.zeros(32, np.uint32)))
+    x = np.full((batch, dims[0]), 3.0e38, np.float32)
+    mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, np.zeros(batch, np.uint32)))
     assert mlp.overflow()
     for a, b in zip(w0, mlp.weights()):
         assert np.array_equal(a, b)
-    x = normal_batch(1, 32, 64)
-    mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, uniform_labels(2, 32, 10)))
+    x = normal_batch(1, batch, dims[0])
+    mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, uniform_labels(2, batch, dims[-1])))
     assert not mlp.overflow()
     assert any(not np.array_equal(a, b) for a, b in zip(w0, mlp.weights()))
