@@ -285,10 +285,10 @@ int rt_empty(rt_ctx* ctx, rt_dtype dtype, const size_t* shape, int rank, rt_buf*
 /* GpuMlp::carregar (mod.rs:1486-1495), overlapped: rt_mlp_load copies a host
  * batch (x in the plan's input dtype: f32, or bf16 bits under RT_PREC_BF16;
  * n = batch labels) into pinned staging and starts its host-to-device copy
- * on a copy stream, into one of two device slots that alternate.  The copy
- * waits only for the last step that read the same slot, so it runs while
- * the step on the other slot computes.  The host buffers may be reused on
- * return.  rt_mlp_step_loaded runs rt_mlp_step on the most recently loaded
+ * on a copy stream, into one of two device slots that alternate.  The call
+ * first waits (on the host) for the last step that read the same slot, two
+ * steps back, so the copy runs while the step on the other slot computes.
+ * The host buffers may be reused on return.  rt_mlp_step_loaded runs rt_mlp_step on the most recently loaded
  * batch after its copy; it may be called again on the same batch. */
 int rt_mlp_load(rt_mlp* mlp, const void* x, size_t x_bytes, const uint64_t* labels, size_t n);
 int rt_mlp_step_loaded(rt_mlp* mlp);

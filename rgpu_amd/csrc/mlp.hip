@@ -659,9 +659,11 @@ int rt_mlp_load(rt_mlp* p, const void* x, size_t x_bytes, const uint64_t* labels
   if (s.copy_pending) HIP_TRY(c, hipEventSynchronize(s.copied), "staging wait");
   std::memcpy(s.x_host, x, x_bytes);
   for (size_t i = 0; i < n; ++i) s.y_host[i] = (uint32_t)labels[i];
-  // The device slot is free once the last step that read it has run; steps
-  // on the other slot run meanwhile (the overlap).
-  if (s.use_pending) HIP_TRY(c, hipStreamWaitEvent(c->copy_stream, s.used, 0), "slot wait");
+  // The device slot is free once the last step that read it has run (two
+  // steps back); the step on the other slot runs meanwhile (the overlap).
+  // The wait is on the host: a copy-engine queue made to wait on the compute
+  // queue starts late (measured: 0.33 vs 0.21 ms per batch-2048 step).
+  if (s.use_pending) HIP_TRY(c, hipEventSynchronize(s.used), "slot wait");
   HIP_TRY(c, hipMemcpyAsync(s.x.ptr, s.x_host, s.x.bytes, hipMemcpyHostToDevice, c->copy_stream), "batch copy");
   HIP_TRY(c, hipMemcpyAsync(s.y.ptr, s.y_host, s.y.bytes, hipMemcpyHostToDevice, c->copy_stream), "label copy");
   HIP_TRY(c, hipEventRecord(s.copied, c->copy_stream), "copy event");
