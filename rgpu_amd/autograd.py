@@ -41,8 +41,8 @@ from typing import Callable, Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
-from .gpu import (LOSS_BCE, LOSS_MAE, LOSS_SOFTMAX_XENT, NN, NT, TN, Gpu, GpuTensor, RtError,
-                  upload_labels)
+from .gpu import (EPI_BIAS, EPI_BIAS_RELU, LOSS_BCE, LOSS_MAE, LOSS_SOFTMAX_XENT, NN, NT, TN, Gpu, GpuTensor,
+                  RtError, upload_labels)
 
 Shape = Tuple[int, ...]
 
@@ -576,15 +576,53 @@ def apply_activation(z: Var, activation) -> Var:
     raise ValueError(f"unknown activation {activation!r}")
 
 
+def dense_node(x: Var, w: Var, b: Var, relu: bool) -> Var:
+    """A = φ(X W + 1ₙ b) for φ = relu or linear as ONE tape node: the GEMM
+    applies the bias (and ReLU) in its epilogue, whose arithmetic is the
+    reference's matmul, add and relu in sequence (acc + b, then max(·, 0)),
+    so the values are the same bits.  Backward: δ = ḡ ⊙ 1[A > 0] (A > 0
+    exactly where Z > 0), dW = Xᵀδ with db = 1ᵀδ summed in the same launch,
+    dX = δ Wᵀ — three launches where the node-per-op tape takes four, and one
+    forward launch instead of three.  db is summed in the GEMM's order, not
+    reduce_to's row order: equal within rounding, not bit for bit."""
+    gpu = x.gpu
+    xv, wv, bv = x.value, w.value, b.value
+    (m, k), (k2, n) = xv.shape, wv.shape
+    if k != k2 or bv.shape not in ((1, n), (n,)):
+        raise ValueError(f"dense: {xv.shape} x {wv.shape} + {bv.shape}")
+    a = gpu.empty((m, n))
+    gpu.gemm(NN, xv, wv, a, EPI_BIAS_RELU if relu else EPI_BIAS, bv)
+
+    def bw(g):
+        if relu:
+            d = gpu.empty((m, n))
+            gpu.map_vjp("relu", g, a, None, d)
+        else:
+            d = g
+        dx, dw, db = gpu.empty((m, k)), gpu.empty((k, n)), gpu.empty(bv.shape)
+        gpu.gemm(TN, xv, d, dw, colsum=db)
+        gpu.gemm(NT, d, wv, dx)
+        return dx, dw, db
+
+    if x.tape is not w.tape or w.tape is not b.tape:
+        raise ValueError("operands belong to different tapes")
+    idx = x.tape._push((x.idx, w.idx, b.idx), bw)
+    return Var(x.tape, idx, a)
+
+
 class Dense:
     """nn.rs:108-159: A = φ(X W + 1ₙ b), W [inputs, units], b [1, units].
 
     The Glorot-uniform draw (nn.rs:122-130) takes its numbers from ``rng``,
     any object with ``range(lo, hi)`` (or a vectorised ``ranges(n, lo, hi)``)
-    that follows rtensor's Rng; or pass ``weights`` / ``bias`` directly."""
+    that follows rtensor's Rng; or pass ``weights`` / ``bias`` directly.
+    With ``fused`` (the default) a ReLU or linear layer is one tape node
+    (``dense_node``); ``fused=False`` records matmul, add and the activation
+    as the reference does."""
 
     def __init__(self, gpu: Gpu, inputs: int, units: int, activation="linear", rng=None,
-                 weights=None, bias=None):
+                 weights=None, bias=None, fused: bool = True):
+        self.fused = fused
         if weights is None:
             if rng is None:
                 raise ValueError("Dense needs an rng or explicit weights")
@@ -609,7 +647,11 @@ class Dense:
 
     def forward(self, x: Var) -> Var:
         t = x.tape
-        z = x.matmul(self.w.watch(t)).add(self.b.watch(t))
+        w, b = self.w.watch(t), self.b.watch(t)
+        kind, _ = _activation(self.activation)
+        if self.fused and kind in ("relu", "linear") and len(x.shape) == 2:
+            return dense_node(x, w, b, kind == "relu")
+        z = x.matmul(w).add(b)
         return apply_activation(z, self.activation)
 
     def params(self) -> List[Param]:

@@ -590,3 +590,30 @@ def test_optimizer_updates_a_repeated_parameter_twice(gpu):
         t.watch(wo).square().sum().backward()
         oo.step([wo, wo], t)
     assert bits_equal(w.value(), wo.value())
+
+
+@pytest.mark.parametrize("act", ["relu", "linear"])
+def test_fused_dense_node_matches_op_by_op(gpu, act):
+    """dense_node (GEMM with bias/ReLU epilogue, colsum-fused db) against the
+    reference's matmul -> add -> relu recording: same forward bits, same dX
+    and dW bits (the same GEMM calls), db within rounding."""
+    r = np.random.default_rng(21)
+    x = r.standard_normal((96, 40)).astype(np.float32)
+    w = r.standard_normal((40, 72)).astype(np.float32) * np.float32(0.2)
+    b = r.standard_normal((1, 72)).astype(np.float32)
+    gup = r.standard_normal((96, 72)).astype(np.float32)
+    outs = []
+    for fused in (True, False):
+        layer = A.Dense(gpu, 40, 72, act, weights=w, bias=b, fused=fused)
+        t = A.Tape(gpu)
+        px = A.Param(gpu, "x", x)
+        y = layer.forward(px.watch(t))
+        grads = y.mul(t.constant(gup)).sum().backward()
+        outs.append((y.numpy(), gpu.download(grads.of(px)), gpu.download(grads.of(layer.w)),
+                     gpu.download(grads.of(layer.b)), len(t)))
+    (yf, dxf, dwf, dbf, nf), (yu, dxu, dwu, dbu, nu) = outs
+    assert nf < nu  # fewer tape nodes
+    assert bits_equal(yf, yu)
+    assert bits_equal(dxf, dxu)
+    assert bits_equal(dwf, dwu)
+    assert O.erro_rel(dbf, dbu) <= 1e-6
