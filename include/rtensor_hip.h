@@ -236,10 +236,12 @@ typedef enum {
 typedef enum { RT_B_ADD = 0, RT_B_SUB = 1, RT_B_MUL = 2, RT_B_DIV = 3 } rt_binary_op;
 
 typedef enum {
-  RT_LOSS_MAE = 1,          /* losses.rs:46-53, on d = pred - target       */
-  RT_LOSS_SOFTMAX_XENT = 2, /* losses.rs:99-115, on p = softmax_rows(z)    */
-  RT_LOSS_BCE = 3           /* losses.rs:143-162, on probabilities         */
-} rt_loss_kind;             /* mse (losses.rs:31-34) is sub, square, mean   */
+  RT_LOSS_MAE = 1,                 /* losses.rs:46-53, on d = pred - target        */
+  RT_LOSS_SOFTMAX_XENT = 2,        /* losses.rs:99-115, on p = softmax_rows(z)     */
+  RT_LOSS_BCE = 3,                 /* losses.rs:143-162, on probabilities          */
+  RT_LOSS_SOFTMAX_XENT_LOGITS = 4  /* losses.rs:99-115 on the logits z: softmax,
+                                      loss and dir in one pass per row            */
+} rt_loss_kind;                    /* mse (losses.rs:31-34) is sub, square, mean    */
 
 /* Tensor::map (tensor.rs:160-181) with the forward closure of op:
  * y = f(x), same element count. */
@@ -274,7 +276,9 @@ int rt_softmax_rows_vjp(rt_ctx* ctx, const rt_buf* s, const rt_buf* g, rt_buf* d
  * batch (batch = rows of p for softmax-xent, len(p) otherwise); dir (NULL to
  * skip) = sign(d), p − y, or (c − y)/(c(1 − c)) with c = clamp(p, 1e-7,
  * 1 − 1e-7).  The loss node's VJP is rt_fill_scaled(g, batch, dir).  y is
- * NULL for RT_LOSS_MAE (p is already pred − target). */
+ * NULL for RT_LOSS_MAE (p is already pred − target).  RT_LOSS_SOFTMAX_XENT_LOGITS
+ * takes the logits as p and needs dir; its row sums are added before the
+ * tree, so its value may differ from RT_LOSS_SOFTMAX_XENT's in the last bits. */
 int rt_loss(rt_ctx* ctx, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_buf* value, rt_buf* dir);
 
 /* Gpu::zeros without the zero fill (contents undefined), for op outputs

@@ -41,7 +41,7 @@ from typing import Callable, Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
-from .gpu import (EPI_BIAS, EPI_BIAS_RELU, LOSS_BCE, LOSS_MAE, LOSS_SOFTMAX_XENT, NN, NT, TN, Gpu, GpuTensor,
+from .gpu import (EPI_BIAS, EPI_BIAS_RELU, LOSS_BCE, LOSS_MAE, LOSS_SOFTMAX_XENT_LOGITS, NN, NT, TN, Gpu, GpuTensor,
                   RtError, upload_labels)
 
 Shape = Tuple[int, ...]
@@ -78,12 +78,16 @@ def _as_device(gpu: Gpu, v) -> GpuTensor:
     return gpu.upload(np.ascontiguousarray(v, dtype=np.float32))
 
 
-def _one(gpu: Gpu) -> GpuTensor:
-    """A one-element device tensor holding 1.0, kept on the Gpu object."""
-    t = getattr(gpu, "_autograd_one", None)
+def _ones(gpu: Gpu, shape) -> GpuTensor:
+    """A device tensor of ones of this shape, uploaded once and kept on the
+    Gpu object (the seed of backward; never written)."""
+    cache = getattr(gpu, "_autograd_ones", None)
+    if cache is None:
+        cache = gpu._autograd_ones = {}
+    key = tuple(int(d) for d in shape)
+    t = cache.get(key)
     if t is None or not t.handle:
-        t = gpu.upload(np.ones((), np.float32))
-        gpu._autograd_one = t
+        t = cache[key] = gpu.upload(np.ones(key, np.float32))
     return t
 
 
@@ -345,9 +349,8 @@ class Var:
         nodes = self.tape.nodes
         grads: List[Optional[GpuTensor]] = [None] * len(nodes)
         shared = [False] * len(nodes)
-        seed = gpu.empty(self.shape)
-        gpu.fill_scaled(_one(gpu), seed)
-        grads[self.idx] = seed
+        grads[self.idx] = _ones(gpu, self.shape)  # shared: accumulated into out of place
+        shared[self.idx] = True
         for i in range(len(nodes) - 1, -1, -1):
             parents, backward = nodes[i]
             g = grads[i]
@@ -432,10 +435,8 @@ def softmax_cross_entropy(logits: Var, targets) -> Var:
     y = _as_device(gpu, targets)
     if tuple(y.shape) != tuple(logits.shape):
         raise ValueError("logits and targets differ in shape")
-    probs = gpu.empty(logits.shape)
-    gpu.softmax_rows(logits.value, probs)
     value, dirn = gpu.empty(()), gpu.empty(logits.shape)
-    gpu.loss(LOSS_SOFTMAX_XENT, probs, y, value, dirn)
+    gpu.loss(LOSS_SOFTMAX_XENT_LOGITS, logits.value, y, value, dirn)  # softmax, loss and P − Y in one launch
     batch = float(np.float32(logits.shape[0]))
 
     def bw(g):

@@ -167,8 +167,10 @@ __global__ __launch_bounds__(256) void reduce_to_kernel(const float* __restrict_
 // Fixed-order two-stage sum of n floats: block b adds its 256 x chunk
 // elements (each thread strided, then a shared-memory tree); stage 2 adds
 // the block sums in order and divides by `div`.
+// With a single block (n <= 65536) stage 1 also finishes the sum: out[0] =
+// (0 + block sum) / div, the value stage 2 would produce from one part.
 __global__ __launch_bounds__(256) void sum_stage1(const float* __restrict__ x, long long n, long long chunk,
-                                                  float* __restrict__ part) {
+                                                  float* __restrict__ part, float div, float* __restrict__ out) {
   __shared__ float sh[256];
   const long long b0 = blockIdx.x * chunk, b1 = min(n, b0 + chunk);
   float acc = 0.0f;
@@ -179,7 +181,10 @@ __global__ __launch_bounds__(256) void sum_stage1(const float* __restrict__ x, l
     if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) part[blockIdx.x] = sh[0];
+  if (threadIdx.x == 0) {
+    if (gridDim.x == 1) out[0] = (0.0f + sh[0]) / div;
+    else part[blockIdx.x] = sh[0];
+  }
 }
 
 __global__ void sum_stage2(const float* __restrict__ part, int parts, float div, float* __restrict__ out) {
@@ -255,6 +260,49 @@ __global__ __launch_bounds__(256) void loss_terms_kernel(int kind, const float* 
         break;
       }
     }
+  }
+}
+
+// losses.rs:99-115 from the logits in one pass per row (one thread per row):
+// the softmax of tensor.rs:455-472 (max, exp into dir, sequential sum,
+// divide), then dir = p − y and the row's loss terms −y·ln(max(p, 1e-12))
+// (y ≠ 0) added in column order.  The row sums are added by a block tree;
+// with one block the launch also writes value = (0 + total) / div, else each
+// block writes its part for sum_stage2.
+__global__ __launch_bounds__(256) void xent_logits_kernel(const float* __restrict__ z, const float* __restrict__ y,
+                                                          float* __restrict__ dir, long long rows, long long cols,
+                                                          float* __restrict__ part, float div,
+                                                          float* __restrict__ out) {
+  __shared__ float sh[256];
+  const long long i = blockIdx.x * 256LL + threadIdx.x;
+  float row_term = 0.0f;
+  if (i < rows) {
+    const float* zr = z + i * cols;
+    const float* yr = y + i * cols;
+    float* d = dir + i * cols;
+    float mx = -INFINITY;
+    for (long long j = 0; j < cols; ++j) mx = fmaxf(mx, zr[j]);
+    float sum = 0.0f;
+    for (long long j = 0; j < cols; ++j) {
+      const float e = expf(zr[j] - mx);
+      d[j] = e;
+      sum += e;
+    }
+    for (long long j = 0; j < cols; ++j) {
+      const float pj = d[j] / sum, yj = yr[j];
+      if (yj != 0.0f) row_term += -(yj * logf(fmaxf(pj, 1e-12f)));
+      d[j] = pj - yj;
+    }
+  }
+  sh[threadIdx.x] = row_term;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (gridDim.x == 1) out[0] = (0.0f + sh[0]) / div;
+    else part[blockIdx.x] = sh[0];
   }
 }
 
@@ -375,8 +423,8 @@ size_t sum_scratch_elems(long long n) { return (size_t)std::max<long long>(1, st
 hipError_t sum_all_launch(hipStream_t s, const float* x, long long n, float div, float* out, float* scratch) {
   const long long parts = (long long)sum_scratch_elems(n);
   const long long chunk = std::max<long long>(1, (n + parts - 1) / parts);
-  hipLaunchKernelGGL(sum_stage1, dim3((unsigned)parts), dim3(256), 0, s, x, n, chunk, scratch);
-  hipLaunchKernelGGL(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)parts, div, out);
+  hipLaunchKernelGGL(sum_stage1, dim3((unsigned)parts), dim3(256), 0, s, x, n, chunk, scratch, div, out);
+  if (parts > 1) hipLaunchKernelGGL(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)parts, div, out);
   return hipGetLastError();
 }
 
@@ -397,6 +445,16 @@ hipError_t softmax_rows_vjp_launch(hipStream_t s, const float* sm, const float* 
   if (rows <= 0) return hipSuccess;
   hipLaunchKernelGGL(softmax_rows_vjp_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, sm, g, dx, rows,
                      cols);
+  return hipGetLastError();
+}
+
+hipError_t xent_logits_launch(hipStream_t s, const float* z, const float* y, float* dir, long long rows,
+                              long long cols, float div, float* out, float* scratch, size_t scratch_elems) {
+  const long long blocks = std::max<long long>(1, (rows + 255) / 256);
+  if (blocks > 1 && (size_t)blocks > scratch_elems) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(xent_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, z, y, dir, rows, cols, scratch, div,
+                     out);
+  if (blocks > 1) hipLaunchKernelGGL(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)blocks, div, out);
   return hipGetLastError();
 }
 
@@ -600,7 +658,8 @@ int rt_softmax_rows_vjp(rt_ctx* c, const rt_buf* s, const rt_buf* g, rt_buf* dx)
 int rt_loss(rt_ctx* c, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_buf* value, rt_buf* dir) {
   CHECK_CTX(c);
   if (!p || !value) return fail(c, RT_ERR_INVALID, "null buffer");
-  if (kind != RT_LOSS_MAE && kind != RT_LOSS_SOFTMAX_XENT && kind != RT_LOSS_BCE)
+  if (kind != RT_LOSS_MAE && kind != RT_LOSS_SOFTMAX_XENT && kind != RT_LOSS_BCE &&
+      kind != RT_LOSS_SOFTMAX_XENT_LOGITS)
     return fail(c, RT_ERR_INVALID, "unknown loss kind %d", (int)kind);
   if (kind != RT_LOSS_MAE && !y) return fail(c, RT_ERR_INVALID, "this loss needs targets");
   if (!is_f32(p) || !is_f32(value) || (y && !is_f32(y)) || (dir && !is_f32(dir)))
@@ -609,6 +668,22 @@ int rt_loss(rt_ctx* c, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_b
   if (y && y->n != p->n) return fail(c, RT_ERR_SHAPE, "predictions and targets differ in size");
   if (dir && dir->n != p->n) return fail(c, RT_ERR_SHAPE, "dir must match the predictions");
   float batch = (float)p->n;
+  if (kind == RT_LOSS_SOFTMAX_XENT_LOGITS) {
+    if (p->rank != 2 || y->rank != 2 || y->shape[0] != p->shape[0] || y->shape[1] != p->shape[1])
+      return fail(c, RT_ERR_SHAPE, "logits and targets differ in shape");  // losses.rs:100
+    if (!dir) return fail(c, RT_ERR_INVALID, "the logits form writes dir (it holds the softmax on the way)");
+    const long long rows = (long long)p->shape[0], cols = (long long)p->shape[1];
+    const size_t blocks = (size_t)std::max<long long>(1, (rows + 255) / 256);
+    int rc = ensure_scratch(c, blocks);
+    if (rc) return rc;
+    Launch L(c, "loss");
+    HIP_TRY(c,
+            xent_logits_launch(c->stream, static_cast<const float*>(p->ptr), static_cast<const float*>(y->ptr),
+                               static_cast<float*>(dir->ptr), rows, cols, (float)rows, static_cast<float*>(value->ptr),
+                               c->scratch, c->scratch_elems),
+            "softmax-xent");
+    return RT_OK;
+  }
   if (kind == RT_LOSS_SOFTMAX_XENT) {
     if (p->rank != 2) return fail(c, RT_ERR_SHAPE, "softmax cross-entropy takes [batch, classes]");
     if (y->rank != 2 || y->shape[0] != p->shape[0] || y->shape[1] != p->shape[1])

@@ -617,3 +617,22 @@ def test_fused_dense_node_matches_op_by_op(gpu, act):
     assert bits_equal(dxf, dxu)
     assert bits_equal(dwf, dwu)
     assert O.erro_rel(dbf, dbu) <= 1e-6
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 3), (256, 10), (257, 10), (3000, 33)])
+def test_xent_from_logits_matches_probability_form(gpu, rows, cols):
+    """RT_LOSS_SOFTMAX_XENT_LOGITS (one pass per row) against softmax_rows +
+    RT_LOSS_SOFTMAX_XENT: the same P − Y bits, the value within rounding."""
+    r = np.random.default_rng(rows + cols)
+    z = (r.standard_normal((rows, cols)) * 4).astype(np.float32)
+    y = A.one_hot(r.integers(0, cols, rows), cols)
+    zd, yd = gpu.upload(z), gpu.upload(y)
+    probs = gpu.empty((rows, cols))
+    gpu.softmax_rows(zd, probs)
+    v1, d1 = gpu.empty(()), gpu.empty((rows, cols))
+    gpu.loss(G.LOSS_SOFTMAX_XENT, probs, yd, v1, d1)
+    v2, d2 = gpu.empty(()), gpu.empty((rows, cols))
+    gpu.loss(G.LOSS_SOFTMAX_XENT_LOGITS, zd, yd, v2, d2)
+    assert bits_equal(gpu.download(d1), gpu.download(d2))
+    a, b = float(gpu.download(v1)), float(gpu.download(v2))
+    assert abs(a - b) <= 1e-6 * max(1.0, abs(a))
