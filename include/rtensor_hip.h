@@ -110,6 +110,15 @@ int rt_convert(rt_ctx* ctx, const rt_buf* src, rt_buf* dst);
 int rt_gemm(rt_ctx* ctx, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* c,
             rt_epilogue epi, const rt_buf* aux, rt_buf* colsum);
 
+/* The backward of a Linear layer Z = X·W + 1ₙb (nn.rs:82-98 adjoints; the
+ * op_matmul_at_b + op_matmul_a_bt + ops_colsum of GpuMlp's backward,
+ * mod.rs:1432-1467): dW = Xᵀ·δ [K, N], db = 1ᵀ·δ [N] (NULL to skip) and
+ * dX = δ·Wᵀ [M, K] (NULL to skip), with X [M, K], δ [M, N], W [K, N].  f32
+ * shapes the paired kernel takes run as ONE launch; anything else is the two
+ * rt_gemm calls. */
+int rt_linear_backward(rt_ctx* ctx, const rt_buf* x, const rt_buf* delta, const rt_buf* w, rt_buf* dx, rt_buf* dw,
+                       rt_buf* db);
+
 /* ops_split_k (mod.rs:1095-1146): C = A·B (RT_NN) or Aᵀ·B (RT_TN) with K cut
  * into `slices`; slice s writes partials[s] and a fixed-order reduction sums
  * them (deterministic, no atomics).  partials is f32 with >= slices*M*N

@@ -583,8 +583,8 @@ def dense_node(x: Var, w: Var, b: Var, relu: bool) -> Var:
     reference's matmul, add and relu in sequence (acc + b, then max(·, 0)),
     so the values are the same bits.  Backward: δ = ḡ ⊙ 1[A > 0] (A > 0
     exactly where Z > 0), dW = Xᵀδ with db = 1ᵀδ summed in the same launch,
-    dX = δ Wᵀ — three launches where the node-per-op tape takes four, and one
-    forward launch instead of three.  db is summed in the GEMM's order, not
+    dX = δ Wᵀ — the ReLU VJP and one paired GEMM launch where the node-per-op
+    tape takes four, and one forward launch instead of three.  db is summed in the GEMM's order, not
     reduce_to's row order: equal within rounding, not bit for bit."""
     gpu = x.gpu
     xv, wv, bv = x.value, w.value, b.value
@@ -601,8 +601,7 @@ def dense_node(x: Var, w: Var, b: Var, relu: bool) -> Var:
         else:
             d = g
         dx, dw, db = gpu.empty((m, k)), gpu.empty((k, n)), gpu.empty(bv.shape)
-        gpu.gemm(TN, xv, d, dw, colsum=db)
-        gpu.gemm(NT, d, wv, dx)
+        gpu.linear_backward(xv, d, wv, dx, dw, db)  # TN + colsum and NT, one launch where it can
         return dx, dw, db
 
     if x.tape is not w.tape or w.tape is not b.tape:

@@ -468,6 +468,54 @@ int rt_gemm(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_bu
   return RT_OK;
 }
 
+int rt_linear_backward(rt_ctx* c, const rt_buf* x, const rt_buf* delta, const rt_buf* w, rt_buf* dx, rt_buf* dw,
+                       rt_buf* db) {
+  CHECK_CTX(c);
+  if (!x || !delta || !w || !dw) return fail(c, RT_ERR_INVALID, "null buffer");
+  if (x->rank != 2 || delta->rank != 2 || w->rank != 2) return fail(c, RT_ERR_SHAPE, "linear backward takes rank 2");
+  const size_t m = x->shape[0], k = x->shape[1], n = w->shape[1];
+  if (delta->shape[0] != m || delta->shape[1] != n || w->shape[0] != k)
+    return fail(c, RT_ERR_SHAPE, "x [%zu,%zu], delta [%zu,%zu], w [%zu,%zu] do not chain", m, k, delta->shape[0],
+                delta->shape[1], w->shape[0], n);
+  const bool f32 = x->dtype == RT_F32 && delta->dtype == RT_F32 && w->dtype == RT_F32;
+  const bool outs_f32 = dw->dtype == RT_F32 && (!dx || dx->dtype == RT_F32) && (!db || db->dtype == RT_F32);
+  if (f32 && outs_f32 && dx && dw->n == k * n && dx->n == m * k && (!db || db->n == n) && m && n && k &&
+      m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX) {
+    GemmDesc d0;  // dW = Xᵀ·δ (+ db = 1ᵀδ)
+    d0.layout = RT_TN;
+    d0.A = x->ptr;
+    d0.B = delta->ptr;
+    d0.C = dw->ptr;
+    d0.M = (int)k;
+    d0.N = (int)n;
+    d0.K = (int)m;
+    d0.lda = (int)k;
+    d0.ldb = (int)n;
+    d0.ldc = (int)n;
+    d0.colsum = db ? static_cast<float*>(db->ptr) : nullptr;
+    GemmDesc d1;  // dX = δ·Wᵀ
+    d1.layout = RT_NT;
+    d1.A = delta->ptr;
+    d1.B = w->ptr;
+    d1.C = dx->ptr;
+    d1.M = (int)m;
+    d1.N = (int)k;
+    d1.K = (int)n;
+    d1.lda = (int)n;
+    d1.ldb = (int)n;
+    d1.ldc = (int)k;
+    if (gemm_pair_supported(d0, d1)) {
+      Launch L(c, "linear_bwd");
+      HIP_TRY(c, gemm_pair_launch(c->stream, d0, d1), "linear backward");
+      return RT_OK;
+    }
+  }
+  // Otherwise the two GEMMs one after the other (rt_gemm checks the rest).
+  int rc = rt_gemm(c, RT_TN, x, delta, dw, RT_EPI_NONE, nullptr, db);
+  if (rc == RT_OK && dx) rc = rt_gemm(c, RT_NT, delta, w, dx, RT_EPI_NONE, nullptr, nullptr);
+  return rc;
+}
+
 size_t rt_splitk_slices(size_t m, size_t n, size_t k) {
   // Split only when the output tiles alone cannot fill the 256 CUs: aim for
   // ~512 workgroups (two per CU), keep at least 4 K steps of 32 per slice,

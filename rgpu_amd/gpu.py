@@ -115,6 +115,7 @@ SIGNATURES = {
     "rt_empty": (C.c_int, [_VP, C.c_int, _SZP, C.c_int, C.POINTER(_VP)]),
     "rt_adam_many": (C.c_int, [_VP, C.c_int, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP),
                                C.c_float, C.c_float, C.c_float, C.c_float, C.c_int]),
+    "rt_linear_backward": (C.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP]),
     "rt_mlp_load": (C.c_int, [_VP, _VP, C.c_size_t, C.POINTER(C.c_uint64), C.c_size_t]),
     "rt_mlp_step_loaded": (C.c_int, [_VP]),
     "rt_sgd_many": (C.c_int, [_VP, C.c_int, C.POINTER(_VP), C.POINTER(_VP), C.POINTER(_VP), C.c_float, C.c_float]),
@@ -321,6 +322,12 @@ class Gpu:
         """ops_split_k (mod.rs:1095-1146)."""
         self._call("rt_gemm_splitk", self._h, TN if transposta else NN, a.handle, b.handle, c.handle,
                    partials.handle, slices, colsum.handle if colsum else None)
+
+    def linear_backward(self, x, delta, w, dx, dw, db=None):
+        """dW = Xᵀδ, db = 1ᵀδ, dX = δWᵀ of a Linear layer (one launch when the
+        paired kernel takes the shapes)."""
+        self._call("rt_linear_backward", self._h, x.handle, delta.handle, w.handle,
+                   dx.handle if dx is not None else None, dw.handle, db.handle if db is not None else None)
 
     def colsum(self, src, dst):
         self._call("rt_colsum", self._h, src.handle, dst.handle)

@@ -370,3 +370,26 @@ def test_region_timer(gpu):
     assert np.all(gpu.download(c) == 256.0)
     with pytest.raises(G.RtError):
         gpu.timer_end()  # no region open
+
+
+@pytest.mark.parametrize("m,k,n,dt", [(256, 128, 512, G.F32), (256, 512, 10, G.F32), (200, 96, 72, G.F32),
+                                      (256, 256, 128, G.BF16)])
+def test_linear_backward_matches_separate_gemms(gpu, m, k, n, dt):
+    """rt_linear_backward (one paired launch where it can) gives the bits of
+    rt_gemm TN with the fused colsum plus rt_gemm NT; dx may be skipped."""
+    r = np.random.default_rng(m + k + n)
+    x = gpu.upload(r.standard_normal((m, k)).astype(np.float32), dt)
+    d = gpu.upload(r.standard_normal((m, n)).astype(np.float32), dt)
+    w = gpu.upload(r.standard_normal((k, n)).astype(np.float32), dt)
+    dx1, dw1, db1 = gpu.zeros((m, k)), gpu.zeros((k, n)), gpu.zeros((1, n))
+    gpu.linear_backward(x, d, w, dx1, dw1, db1)
+    dx2, dw2, db2 = gpu.zeros((m, k)), gpu.zeros((k, n)), gpu.zeros((1, n))
+    gpu.gemm(G.TN, x, d, dw2, colsum=db2)
+    gpu.gemm(G.NT, d, w, dx2)
+    for a, b in ((dx1, dx2), (dw1, dw2), (db1, db2)):
+        assert np.array_equal(gpu.download(a).view(np.uint32), gpu.download(b).view(np.uint32))
+    dw3 = gpu.zeros((k, n))
+    gpu.linear_backward(x, d, w, None, dw3, None)
+    assert np.array_equal(gpu.download(dw3).view(np.uint32), gpu.download(dw2).view(np.uint32))
+    with pytest.raises(G.RtError):
+        gpu.linear_backward(x, d, gpu.zeros((k + 1, n)), dx1, dw1, db1)
