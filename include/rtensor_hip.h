@@ -150,7 +150,9 @@ int rt_sgd(rt_ctx* ctx, rt_buf* theta, rt_buf* velocity, const rt_buf* g, float 
 /* Adam::step / Sgd::step over a whole parameter list (optim.rs:80-114,
  * 162-198: the loop over params), as one launch per 24 tensors instead of
  * one per tensor.  Arrays of n buffers; for SGD without momentum velocity
- * may be NULL.  Arithmetic identical to rt_adam / rt_sgd. */
+ * may be NULL.  Arithmetic identical to rt_adam / rt_sgd.  A tensor listed
+ * again is updated again, after its earlier listing (the repeat starts a new
+ * launch), as the loop over the list would. */
 int rt_adam_many(rt_ctx* ctx, int n, rt_buf* const* theta, rt_buf* const* m, rt_buf* const* v,
                  const rt_buf* const* g, float lr, float beta1, float beta2, float eps, int t);
 int rt_sgd_many(rt_ctx* ctx, int n, rt_buf* const* theta, rt_buf* const* velocity, const rt_buf* const* g,
@@ -314,7 +316,8 @@ int rt_mlp_step_loaded(rt_mlp* mlp);
 int rt_argmax_rows(rt_ctx* ctx, const rt_buf* logits, rt_buf* out);
 
 /* losses::accuracy (losses.rs:181-185): the fraction of rows whose argmax
- * equals the label, hits / B in f32 (0 for B = 0).  labels: u32 [B].
+ * equals the label, hits / B in f32 (NaN for B = 0, as 0/0; 0 for zero
+ * columns, which give no predictions).  labels: u32 [B].
  * Blocking. */
 int rt_accuracy(rt_ctx* ctx, const rt_buf* logits, const rt_buf* labels, float* out);
 

@@ -333,8 +333,10 @@ static Tensor softmax_rows(const Tensor& z) {
 }
 
 // tensor.rs:476-493: first maximum wins ties.
+// One prediction per chunk of max(c, 1) elements (chunks_exact): with zero
+// columns the data is empty and there are no predictions at all.
 static std::vector<size_t> argmax_rows(const Tensor& z) {
-  size_t r = z.shape[0], c = z.shape[1];
+  size_t c = z.shape[1], r = c == 0 ? 0 : z.shape[0];
   std::vector<size_t> out(r, 0);
   for (size_t i = 0; i < r; ++i) {
     size_t best = 0;
@@ -813,6 +815,7 @@ int ocpu_reduce_to(const float* g, size_t r, size_t c, size_t t0, size_t t1, flo
 int ocpu_argmax_rows(const float* z, size_t r, size_t c, uint32_t* out) {
   OC_TRY({
     auto v = argmax_rows(Tensor({r, c}, std::vector<float>(z, z + r * c)));
+    if (v.size() != r) throw std::runtime_error("argmax_rows: zero columns give no predictions");
     for (size_t i = 0; i < r; ++i) out[i] = (uint32_t)v[i];
   });
   return 0;
@@ -820,8 +823,8 @@ int ocpu_argmax_rows(const float* z, size_t r, size_t c, uint32_t* out) {
 // losses.rs:181-185
 float ocpu_accuracy(const float* z, size_t r, size_t c, const uint32_t* labels) {
   auto v = argmax_rows(Tensor({r, c}, std::vector<float>(z, z + r * c)));
-  size_t hits = 0;
-  for (size_t i = 0; i < r; ++i) hits += (v[i] == labels[i]);
+  size_t hits = 0;  // zip of predictions and labels: the shorter one ends it
+  for (size_t i = 0; i < v.size(); ++i) hits += (v[i] == labels[i]);
   return (float)hits / (float)r;
 }
 int ocpu_one_hot(const uint32_t* labels, size_t n, size_t classes, float* out) {

@@ -316,7 +316,7 @@ extern "C" {
 
 int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* const* weights, const float* const* biases,
                   size_t batch, const rt_mlp_config* cfg, rt_mlp** out) {
-  if (c == nullptr) return RT_ERR_INVALID;
+  CHECK_CTX(c);
   if (out == nullptr || dims == nullptr || weights == nullptr || biases == nullptr || cfg == nullptr)
     return fail(c, RT_ERR_INVALID, "null argument");
   *out = nullptr;
@@ -503,6 +503,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
 
 int rt_mlp_destroy(rt_mlp* p) {
   if (p == nullptr) return RT_OK;
+  bind_device(p->ctx);
   auto& v = p->ctx->mlps;
   v.erase(std::remove(v.begin(), v.end(), p), v.end());
   mlp_release(p);
@@ -521,6 +522,7 @@ static int check_inputs(rt_mlp* p, const rt_buf* x) {
 
 int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   int rc = check_inputs(p, x);
   if (rc) return rc;
@@ -645,6 +647,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
 
 int rt_mlp_load(rt_mlp* p, const void* x, size_t x_bytes, const uint64_t* labels, size_t n) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   if (x == nullptr || labels == nullptr) return fail(c, RT_ERR_INVALID, "null batch");
   int rc = ensure_slots(p);
@@ -675,6 +678,7 @@ int rt_mlp_load(rt_mlp* p, const void* x, size_t x_bytes, const uint64_t* labels
 
 int rt_mlp_step_loaded(rt_mlp* p) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   if (p->loaded < 0) return fail(c, RT_ERR_INVALID, "no batch loaded");
   auto& s = p->slot[p->loaded];
@@ -688,6 +692,7 @@ int rt_mlp_step_loaded(rt_mlp* p) {
 
 int rt_mlp_forward(rt_mlp* p, const rt_buf* x) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   int rc = check_inputs(p, x);
   if (rc) return rc;
   return run_forward(p, x, nullptr, 1.0f);
@@ -695,6 +700,7 @@ int rt_mlp_forward(rt_mlp* p, const rt_buf* x) {
 
 int rt_mlp_logits(rt_mlp* p, float* host, size_t n) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   const Layer& top = p->L[p->n_layers - 1];
   if (host == nullptr || n != p->batch * top.dout) return fail(c, RT_ERR_SHAPE, "logits need %zu floats", p->batch * top.dout);
@@ -706,6 +712,7 @@ int rt_mlp_logits(rt_mlp* p, float* host, size_t n) {
 
 int rt_mlp_last_loss(rt_mlp* p, float* out) {
   if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   std::vector<float> rows(p->batch);
   int flag = 0;
@@ -761,6 +768,7 @@ static int put(rt_mlp* p, float* base, const float* const* host, int n) {
 
 int rt_mlp_set_weights(rt_mlp* p, const float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   int rc = put(p, p->theta, host, n);
   if (rc || !p->mixed) return rc;
   rt_ctx* c = p->ctx;
@@ -772,6 +780,7 @@ int rt_mlp_set_weights(rt_mlp* p, const float* const* host, int n) {
 
 int rt_mlp_get_optimizer_state(rt_mlp* p, float* const* m, float* const* v, int n, int* t) {
   if (p == nullptr || t == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   int rc;
   if (m != nullptr && (rc = fetch(p, p->m, m, n))) return rc;
@@ -792,6 +801,7 @@ int rt_mlp_get_optimizer_state(rt_mlp* p, float* const* m, float* const* v, int 
 
 int rt_mlp_set_optimizer_state(rt_mlp* p, const float* const* m, const float* const* v, int n, int t) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   if (t < 0) return fail(c, RT_ERR_INVALID, "t must be >= 0");
   int rc;
@@ -809,11 +819,13 @@ int rt_mlp_set_optimizer_state(rt_mlp* p, const float* const* m, const float* co
 
 int rt_mlp_weights(rt_mlp* p, float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   return fetch(p, p->theta, host, n);
 }
 
 int rt_mlp_grads(rt_mlp* p, float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   int rc = fetch(p, p->grad, host, n);
   if (rc || !p->mixed || p->cfg.loss_scale == 1.0f) return rc;
   // Gradients are held scaled by the loss scale; report dL/dθ.
@@ -828,12 +840,14 @@ int rt_mlp_grads(rt_mlp* p, float* const* host, int n) {
 
 int rt_mlp_dispatches(rt_mlp* p, int* out) {
   if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   *out = p->dispatches;
   return RT_OK;
 }
 
 int rt_mlp_overflow(rt_mlp* p, int* out) {
   if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   int flag = 0;
   hipError_t e = hipMemcpyAsync(&flag, p->state + 1, sizeof(int), hipMemcpyDeviceToHost, c->stream);

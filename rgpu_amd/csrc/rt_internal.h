@@ -68,9 +68,18 @@ int hip_fail(rt_ctx* c, hipError_t e, const char* what);
 // work before replacing a smaller one).
 int ensure_scratch(rt_ctx* c, size_t elems);
 
+// HIP's current device is per thread: every entry point makes the context's
+// device current first, so a context works from any thread and next to a
+// context on another device.
+inline void bind_device(const rt_ctx* c) {
+  int d = -1;
+  if (hipGetDevice(&d) != hipSuccess || d != c->device) hipSetDevice(c->device);
+}
+
 #define CHECK_CTX(c)                           \
   do {                                         \
     if ((c) == nullptr) return RT_ERR_INVALID; \
+    ::rt::bind_device(c);                      \
   } while (0)
 
 #define HIP_TRY(c, expr, what)                                  \

@@ -249,14 +249,15 @@ static int make_buf(rt_ctx* c, rt_dtype dtype, const size_t* shape, int rank, rt
   if (out == nullptr || (rank > 0 && shape == nullptr) || rank < 0 || rank > 4)
     return fail(c, RT_ERR_INVALID, "bad shape arguments");
   if (dtype < RT_F32 || dtype > RT_U32) return fail(c, RT_ERR_DTYPE, "unknown dtype %d", (int)dtype);
+  size_t n = 1;
+  for (int i = 0; i < rank; ++i) {
+    if (shape[i] != 0 && n > (SIZE_MAX >> 4) / shape[i]) return fail(c, RT_ERR_SHAPE, "shape too large");
+    n *= shape[i];
+  }
   auto* b = new rt_buf();
   b->dtype = dtype;
   b->rank = rank;
-  size_t n = 1;
-  for (int i = 0; i < rank; ++i) {
-    b->shape[i] = shape[i];
-    n *= shape[i];
-  }
+  for (int i = 0; i < rank; ++i) b->shape[i] = shape[i];
   b->n = n;
   b->bytes = n * dtype_size(dtype);
   if (b->bytes > 0) {
@@ -683,11 +684,12 @@ int rt_accuracy(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, float* ou
   if (logits->rank != 2 || logits->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "logits must be f32 [B, C]");
   const size_t B = logits->shape[0], Cc = logits->shape[1];
   if (labels->dtype != RT_U32 || labels->n != B) return fail(c, RT_ERR_SHAPE, "labels must be u32 [%zu]", B);
-  if (B == 0) {
-    *out = 0.0f;
+  // hits / labels.len() as the reference computes it: 0/0 = NaN for an empty
+  // batch; zero columns give no predictions, hence no hits.
+  if (B == 0 || Cc == 0) {
+    *out = B == 0 ? std::nanf("") : 0.0f;
     return RT_OK;
   }
-  if (Cc == 0) return fail(c, RT_ERR_SHAPE, "zero classes");
   if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "too large");
   // Predictions in the context scratch (grow-only), then compared on the host.
   int rc = ensure_scratch(c, B);
@@ -707,12 +709,23 @@ int rt_accuracy(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, float* ou
   return RT_OK;
 }
 
-// One launch per kMaxOptTensors tensors of the list.
+// One launch per run of at most kMaxOptTensors tensors.  A tensor listed again
+// starts a new run: the tensors of one launch are updated concurrently, and a
+// repeated one must see its first update before the second, as in a loop over
+// the list.
 static int launch_opt_list(rt_ctx* c, const std::vector<OptTensor>& ts, const OptParams& P) {
-  for (size_t i = 0; i < ts.size(); i += kMaxOptTensors) {
-    const int nt = (int)std::min<size_t>(kMaxOptTensors, ts.size() - i);
+  size_t i = 0;
+  while (i < ts.size()) {
+    size_t j = i + 1;
+    while (j < ts.size() && j - i < (size_t)kMaxOptTensors) {
+      bool repeat = false;
+      for (size_t q = i; q < j && !repeat; ++q) repeat = ts[q].theta == ts[j].theta;
+      if (repeat) break;
+      ++j;
+    }
     Launch L(c, "optimizer");
-    HIP_TRY(c, optimizer_launch(c->stream, ts.data() + i, nt, P), "optimizer");
+    HIP_TRY(c, optimizer_launch(c->stream, ts.data() + i, (int)(j - i), P), "optimizer");
+    i = j;
   }
   return RT_OK;
 }

@@ -578,6 +578,31 @@ def test_multi_tensor_optimizer_matches_per_tensor(gpu, kind):
         assert bits_equal(gpu.download(x), gpu.download(y))
 
 
+@pytest.mark.parametrize("kind", ["adam", "sgd_momentum"])
+def test_multi_tensor_entry_point_orders_a_repeated_tensor(gpu, kind):
+    """rt_adam_many / rt_sgd_many given the same tensor twice in one list
+    update it twice, the second time from the first's result (a new launch
+    starts at the repeat): bit-identical to two single-tensor calls."""
+    r = np.random.default_rng(12)
+    th, gr = r.standard_normal((70, 9)).astype(np.float32), r.standard_normal((70, 9)).astype(np.float32)
+    other = r.standard_normal((5, 5)).astype(np.float32)
+    a, b, g = gpu.upload(th), gpu.upload(th), gpu.upload(gr)
+    o, go = gpu.upload(other), gpu.upload(other)
+    ma, va, mb, vb = gpu.zeros(th.shape), gpu.zeros(th.shape), gpu.zeros(th.shape), gpu.zeros(th.shape)
+    mo, vo = gpu.zeros(other.shape), gpu.zeros(other.shape)
+    for t in (1, 2):
+        if kind == "adam":
+            gpu.adam_many([a, o, a], [ma, mo, ma], [va, vo, va], [g, go, g], 1e-2, t=t)
+            gpu.adam(b, mb, vb, g, 1e-2, t=t)
+            gpu.adam(b, mb, vb, g, 1e-2, t=t)
+        else:
+            gpu.sgd_many([a, o, a], [g, go, g], 0.1, 0.9, [ma, mo, ma])
+            gpu.sgd(b, g, 0.1, 0.9, mb)
+            gpu.sgd(b, g, 0.1, 0.9, mb)
+    assert bits_equal(gpu.download(a), gpu.download(b))
+    assert bits_equal(gpu.download(ma), gpu.download(mb))
+
+
 def test_optimizer_updates_a_repeated_parameter_twice(gpu):
     """A parameter listed twice is stepped twice, one after the other, as in
     the reference's loop over params (optim.rs:167-197)."""

@@ -393,3 +393,55 @@ def test_linear_backward_matches_separate_gemms(gpu, m, k, n, dt):
     assert np.array_equal(gpu.download(dw3).view(np.uint32), gpu.download(dw2).view(np.uint32))
     with pytest.raises(G.RtError):
         gpu.linear_backward(x, d, gpu.zeros((k + 1, n)), dx1, dw1, db1)
+
+
+@pytest.mark.parametrize("dt", [G.F32, G.BF16])
+def test_zero_sized_dimensions(gpu, dt):
+    """Empty inner and outer dimensions as the CPU path treats them: K = 0
+    sums nothing, so C is the epilogue applied to zero (tensor.rs:318-373 with
+    k = 0) and the fused column sums are zero; zero rows or columns launch
+    nothing and leave the outputs alone; output buffers start as garbage."""
+    m, n = 70, 130
+    bias = np.linspace(-1, 1, n, dtype=np.float32).reshape(1, n)
+    junk = np.full((m, n), 7.0, np.float32)
+    a0, b0 = np.zeros((m, 0), np.float32), np.zeros((0, n), np.float32)
+    want = np.maximum(O.matmul(a0, b0) + bias, 0)
+    c = gpu.upload(junk)
+    gpu.gemm(G.NN, gpu.upload(a0, dt), gpu.upload(b0, dt), c, G.EPI_BIAS_RELU, gpu.upload(bias))
+    assert np.array_equal(gpu.download(c), want)
+    # TN with the bias gradient fused, over zero rows of δ
+    c, cs = gpu.upload(junk), gpu.upload(np.full((1, n), 3.0, np.float32))
+    gpu.gemm(G.TN, gpu.upload(np.zeros((0, m), np.float32), dt), gpu.upload(b0, dt), c, colsum=cs)
+    assert np.array_equal(gpu.download(c), O.matmul(a0, b0))
+    assert np.array_equal(gpu.download(cs), O.reduce_to(b0, (1, n)))
+    # split-K over K = 0: every slice is empty, the reduce writes zeros
+    c, cs = gpu.upload(junk), gpu.upload(np.full((1, n), 3.0, np.float32))
+    parts = gpu.upload(np.full((4 * m * n + 4 * n,), 5.0, np.float32))
+    gpu.split_k(gpu.upload(np.zeros((0, m), np.float32), dt), gpu.upload(b0, dt), c, parts, 4, True, colsum=cs)
+    assert not gpu.download(c).any() and not gpu.download(cs).any()
+    # M = 0 and N = 0: nothing to write
+    gpu.gemm(G.NN, gpu.upload(np.zeros((0, 5), np.float32), dt), gpu.upload(np.ones((5, n), np.float32), dt),
+             gpu.zeros((0, n)))
+    gpu.gemm(G.NN, gpu.upload(np.ones((m, 5), np.float32), dt), gpu.upload(np.zeros((5, 0), np.float32), dt),
+             gpu.zeros((m, 0)))
+    gpu.sync()
+
+
+def test_zero_rows_in_row_ops(gpu):
+    """Column sums of zero rows are zero (reduce_to sums nothing); the loss
+    and argmax of an empty batch launch nothing; the accuracy of an empty
+    batch is 0/0 = NaN and of zero columns 0 (no predictions), as
+    losses.rs:181-185 computes them."""
+    cs = gpu.upload(np.full((1, 9), 2.0, np.float32))
+    gpu.colsum(gpu.zeros((0, 9)), cs)
+    assert np.array_equal(gpu.download(cs), O.reduce_to(np.zeros((0, 9), np.float32), (1, 9)))
+    z, lab = gpu.zeros((0, 10)), gpu.upload(np.zeros(0, np.uint32))
+    gpu.softmax_xent(z, lab, gpu.zeros((0, 10)), gpu.zeros((0,)))
+    gpu.argmax_rows(z, gpu.upload(np.zeros(0, np.uint32)))
+    acc = gpu.accuracy(z, lab)
+    assert np.isnan(acc) and np.isnan(O.accuracy(np.zeros((0, 10), np.float32), np.zeros(0, np.uint32)))
+    lab3 = gpu.upload(np.zeros(3, np.uint32))
+    assert gpu.accuracy(gpu.zeros((3, 0)), lab3) == O.accuracy(np.zeros((3, 0), np.float32), np.zeros(3, np.uint32)) == 0.0
+    with pytest.raises(G.RtError):
+        gpu.argmax_rows(gpu.zeros((3, 0)), gpu.upload(np.zeros(3, np.uint32)))
+    gpu.sync()

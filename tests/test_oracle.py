@@ -112,6 +112,17 @@ def test_argmax_nan_and_infinity_cases():
     assert O.argmax_rows(z).tolist() == [0, 2, 0, 0, 0, 2, 0]
 
 
+def test_accuracy_of_empty_inputs():
+    # losses.rs:183-184 divides the hits by labels.len(): an empty batch is
+    # 0/0 = NaN.  argmax_rows walks chunks_exact(c.max(1)) of the data
+    # (tensor.rs:479-480): zero columns leave no data, hence no predictions
+    # and no hits, whatever the labels.
+    assert np.isnan(O.accuracy(np.zeros((0, 4), np.float32), np.zeros(0, np.uint32)))
+    assert O.accuracy(np.zeros((3, 0), np.float32), np.zeros(3, np.uint32)) == 0.0
+    with pytest.raises(RuntimeError):
+        O.argmax_rows(np.zeros((3, 0), np.float32))
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (17, 33, 65), (64, 64, 64), (65, 64, 63), (130, 96, 80),
                                    (199, 130, 71), (256, 512, 128)])
 def test_matmul_against_float64(m, n, k):
