@@ -178,7 +178,8 @@ typedef struct {
 /* GpuMlp::from_params (mod.rs:1341-1482).  n_layers Dense layers with
  * dims[0..n_layers]; weights[l] is host [dims[l], dims[l+1]], biases[l] is
  * host [1, dims[l+1]].  Hidden layers are ReLU and the output is linear, as
- * in the reference plan (mod.rs:1418-1424).  batch fixes the plan's shapes. */
+ * in the reference plan (mod.rs:1418-1424).  batch fixes the plan's shapes.
+ * 1 <= n_layers <= 1024. */
 int rt_mlp_create(rt_ctx* ctx, int n_layers, const size_t* dims, const float* const* weights,
                   const float* const* biases, size_t batch, const rt_mlp_config* cfg, rt_mlp** out);
 int rt_mlp_destroy(rt_mlp* mlp);

@@ -320,7 +320,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   if (out == nullptr || dims == nullptr || weights == nullptr || biases == nullptr || cfg == nullptr)
     return fail(c, RT_ERR_INVALID, "null argument");
   *out = nullptr;
-  if (n_layers < 1 || n_layers > kMaxOptTensors / 2) return fail(c, RT_ERR_INVALID, "n_layers must be in [1, 12]");
+  if (n_layers < 1 || n_layers > 1024) return fail(c, RT_ERR_INVALID, "n_layers must be in [1, 1024]");
   if (batch < 1 || batch > (1u << 30)) return fail(c, RT_ERR_INVALID, "batch must be >= 1");
   if (!valid_cfg(cfg)) return fail(c, RT_ERR_INVALID, "bad rt_mlp_config");
   for (int l = 0; l <= n_layers; ++l)

@@ -73,6 +73,18 @@ def test_training_follows_cpu_trajectory(gpu):  # gpu.rs:99-139
     assert loss < 0.15
 
 
+def test_deep_plan_follows_cpu(gpu):
+    # 15 layers (30 parameter tensors: the optimizer needs two launches of
+    # at most 24 tensors), Adam; the reference's plan takes any depth.  A
+    # float32 numpy run of the same 20 steps (another summation order) stays
+    # within 3e-6 of the oracle's loss and 3e-5 of its weights here; longer
+    # or faster runs of so deep a net amplify order effects past 2e-3.
+    x, lab = quadrant_data()
+    dims = [8] + [32] * 14 + [4]
+    loss, _ = _trajectory(gpu, x, lab, dims, 5, 20, 0.005)
+    assert loss < 0.6
+
+
 def test_narrow_output_layer_uses_split_k_and_follows_cpu(gpu):  # gpu.rs:145-213
     x, lab = quadrant_data(512, 8)
     loss, mlp = _trajectory(gpu, x, lab, [8, 128, 4], 7, 60, 0.05)
