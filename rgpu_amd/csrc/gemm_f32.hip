@@ -646,8 +646,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const long long total = (long long)M * N;
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
        i += (long long)gridDim.x * blockDim.x) {
+    // v = plane 0 + plane 1 + ... in slice order; the loads go out 8 at a
+    // time so the chain of adds does not wait on one load after another.
     float v = part[i];
-    for (int s = 1; s < S; ++s) v += part[s * stride + i];
+    int s = 1;
+    for (; s + 8 <= S; s += 8) {
+      float t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] = part[(long long)(s + j) * stride + i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v += t[j];
+    }
+    for (; s < S; ++s) v += part[(long long)s * stride + i];
     const int row = (int)(i / N), col = (int)(i % N);
     if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) {
       v = v + bias[col];
@@ -660,7 +670,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   if (cs != nullptr) {
     for (long long j = blockIdx.x * (long long)blockDim.x + threadIdx.x; j < N; j += (long long)gridDim.x * blockDim.x) {
       float v = cs_part[j];
-      for (int s = 1; s < S; ++s) v += cs_part[(long long)s * N + j];
+      int s = 1;
+      for (; s + 8 <= S; s += 8) {
+        float t[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) t[q] = cs_part[(long long)(s + q) * N + j];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v += t[q];
+      }
+      for (; s < S; ++s) v += cs_part[(long long)s * N + j];
       cs[j] = v;
     }
   }

@@ -48,11 +48,12 @@ struct Layer {
   void* delta_h = nullptr;      // [batch, dout] bf16 (mixed precision)
   int splits_dw = 1;
   int splits_fwd = 1;
+  int splits_dx = 1;  // dX = δ·Wᵀ of this layer (l > 0)
   bool pair_bwd = false;  // dW and dX of this layer in one launch
   // dW / db split-K planes of this layer summed by the optimizer (f32 plans):
   // [splits_dw][din*dout] then [splits_dw][dout], owned by this layer.
   float* dw_parts = nullptr;
-  std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx, lbl_bwd;
+  std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx, lbl_dx_red, lbl_bwd;
 };
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -96,7 +97,6 @@ struct rt_mlp {
   int dispatches = 0;
   bool mixed = false;
   bool head_fused = false;  // output layer GEMM + softmax-xent in one launch
-  const rt_buf* last_x = nullptr;
 };
 
 static bool valid_cfg(const rt_mlp_config* c) {
@@ -346,15 +346,21 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     Ly.b_off = off;
     off += round_up(Ly.dout, 64);
     const bool last = l == n_layers - 1;
-    // Forward split-K only on the linear output layer (mod.rs:1360-1367):
-    // hidden layers are wide enough, and the ReLU epilogue stays fused.
-    Ly.splits_fwd = last ? (int)rt_splitk_slices(batch, Ly.dout, Ly.din) : 1;
+    // Split-K where the output tiles alone cannot fill the chip: the
+    // output layer's forward (as mod.rs:1360-1367 does) and, at small
+    // batches, the hidden layers' forward and dX too, whose bias+ReLU or
+    // ReLU-mask epilogue then runs in the reduction (f32 plans; the bf16
+    // plan's hidden outputs are bf16, which the reduction does not write).
+    const bool small_ok = last || !p->mixed;
+    Ly.splits_fwd = small_ok ? (int)rt_splitk_slices(batch, Ly.dout, Ly.din) : 1;
+    Ly.splits_dx = (l > 0 && !p->mixed) ? (int)rt_splitk_slices(batch, Ly.din, Ly.dout) : 1;
     Ly.splits_dw = (int)rt_splitk_slices(Ly.din, Ly.dout, batch);
     Ly.lbl_fwd = "fwd_l" + std::to_string(l);
     Ly.lbl_fwd_red = "fwd_reduce_l" + std::to_string(l);
     Ly.lbl_dw = "dw_l" + std::to_string(l);
     Ly.lbl_dw_red = "dw_reduce_l" + std::to_string(l);
     Ly.lbl_dx = "dx_l" + std::to_string(l);
+    Ly.lbl_dx_red = "dx_reduce_l" + std::to_string(l);
     Ly.lbl_bwd = "dwdx_l" + std::to_string(l);
   }
   p->n_params = off;
@@ -366,6 +372,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   for (int l = 0; l < n_layers; ++l) {
     const Layer& Ly = p->L[l];
     if (Ly.splits_fwd > 1) part = std::max(part, (size_t)Ly.splits_fwd * batch * Ly.dout);
+    if (Ly.splits_dx > 1) part = std::max(part, (size_t)Ly.splits_dx * batch * Ly.din);
     if (Ly.splits_dw > 1) {
       const size_t e = (size_t)Ly.splits_dw * (Ly.din * Ly.dout + Ly.dout);
       if (p->mixed) part = std::max(part, e);
@@ -458,7 +465,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     const GemmDesc dx = plan_desc(p, RT_NT, dt, Ly.delta, p->theta + Ly.w_off, p->L[l - 1].delta, RT_F32, (int)batch,
                                   (int)Ly.din, (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr,
                                   p->L[l - 1].act, RT_F32, nullptr, 1);
-    Ly.pair_bwd = gemm_pair_supported(dw, dx);
+    Ly.pair_bwd = Ly.splits_dx == 1 && gemm_pair_supported(dw, dx);
   }
 
   const Layer& top = p->L[n_layers - 1];
@@ -478,7 +485,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
                                     RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
       n += gemm_launch_count(dw) - 1;
     }
-    if (l > 0 && !p->L[l].pair_bwd) n += 1;
+    if (l > 0 && !p->L[l].pair_bwd) n += p->L[l].splits_dx > 1 ? 2 : 1;
   }
   if (!p->head_fused) n += 1;  // softmax-xent
   n += opt_launches(p);  // optimizer
@@ -570,7 +577,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       void* dst = p->mixed ? Lp.delta_h : (void*)Lp.delta;
       const GemmDesc dx = plan_desc(p, RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B, (int)Ly.din,
                                     (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
-                                    p->mixed ? RT_BF16 : RT_F32, nullptr, 1);
+                                    p->mixed ? RT_BF16 : RT_F32, nullptr, Ly.splits_dx);
       if (Ly.pair_bwd) {
         // Both read δ_l and neither feeds the other: one launch.
         Launch Lz(c, Ly.lbl_bwd.c_str());
@@ -582,9 +589,15 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
           hipError_t e = gemm_launch(c->stream, dw);
           if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
         }
-        Launch Lz(c, Ly.lbl_dx.c_str());
-        hipError_t e = gemm_launch(c->stream, dx);
-        if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dx.c_str());
+        {
+          Launch Lz(c, Ly.lbl_dx.c_str());
+          hipError_t e = gemm_launch(c->stream, dx);
+          if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dx.c_str());
+        }
+        // Split dX (small batches): the reduction applies the ReLU mask.
+        rc = finish_split(p, dx, Ly.lbl_dx_red.c_str(), dst, RT_F32, RT_EPI_RELU_MASK, nullptr, Lp.act, RT_F32,
+                          nullptr);
+        if (rc) return rc;
       }
     }
     if (Ly.dw_parts == nullptr) {  // otherwise the optimizer sums the planes
