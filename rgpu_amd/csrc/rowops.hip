@@ -77,7 +77,7 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
 // MFMA step s, and ends with z(rows 4g..4g+3, class r).  The eight partial
 // tiles are added in LDS in wave order; then the 16 lanes of each row run
 // the softmax with width-16 shuffles.  With labels == null only the logits
-// are written.  The K sum order differs from the CPU path's; the rest
+// are written (and bias may be null: z = A·W).  The K sum order differs from the CPU path's; the rest
 // follows xent_kernel.
 typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int HEAD_C = 16, HEAD_ROWS = 16;
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(512) void head_xent_kernel(const float* __restrict_
   float zs = red[0][rr][cc];
 #pragma unroll
   for (int w = 1; w < HW; ++w) zs += red[w][rr][cc];
-  const float z = cc < cols ? zs + bias[cc] : -INFINITY;
+  const float z = cc < cols ? (bias != nullptr ? zs + bias[cc] : zs) : -INFINITY;
   if (row >= rows) return;
   if (cc < cols) logits[(long long)row * cols + cc] = z;
   if (labels == nullptr) return;

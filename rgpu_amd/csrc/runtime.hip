@@ -459,6 +459,19 @@ int rt_gemm(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_bu
     d.mask_dtype = aux->dtype;
   }
   d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
+  // A narrow f32 NN product (an output layer's logits, <= 16 columns) has
+  // too few output tiles for the tiled kernels to be anything but latency
+  // bound; the output-layer kernel splits its K over 8 waves of a block per
+  // 16 rows instead.
+  if (layout == RT_NN && a->dtype == RT_F32 && (epi == RT_EPI_NONE || epi == RT_EPI_BIAS) &&
+      head_xent_supported(d.K, d.N) && d.lda == d.K && (reinterpret_cast<uintptr_t>(d.A) & 15) == 0) {
+    Launch L(c, "gemm_nn");
+    HIP_TRY(c,
+            head_xent_launch(c->stream, static_cast<const float*>(d.A), d.K, static_cast<const float*>(d.B), d.bias,
+                             nullptr, static_cast<float*>(d.C), nullptr, nullptr, d.M, d.N, 0.0f, nullptr),
+            "gemm launch");
+    return RT_OK;
+  }
   if (colsum && is_half(a->dtype)) {
     if ((rc = ensure_scratch(c, colsum_scratch_need(d.M, d.N, 1)))) return rc;
     d.cs_scratch = c->scratch;

@@ -445,3 +445,27 @@ def test_zero_rows_in_row_ops(gpu):
     with pytest.raises(G.RtError):
         gpu.argmax_rows(gpu.zeros((3, 0)), gpu.upload(np.zeros(3, np.uint32)))
     gpu.sync()
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 10, 512), (33, 1, 128), (1000, 16, 384), (5, 7, 1024)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_narrow_f32_product(gpu, m, n, k, bias):
+    """Narrow f32 NN products (<= 16 columns, K a multiple of 128: an output
+    layer's logits) run on the output-layer kernel: as close to the float64
+    product as the oracle's sequential f32 sum is, or 1e-5, and within 1e-4
+    of the oracle (N(0,1) data: sums over K of unit terms)."""
+    r = np.random.default_rng(m + n + k)
+    a, w = r.standard_normal((m, k)).astype(np.float32), r.standard_normal((k, n)).astype(np.float32)
+    b = r.standard_normal((1, n)).astype(np.float32)
+    c = gpu.upload(np.full((m, n), 9.0, np.float32))
+    if bias:
+        gpu.gemm(G.NN, gpu.upload(a), gpu.upload(w), c, G.EPI_BIAS, gpu.upload(b))
+        cpu = O.matmul(a, w) + b
+        exact = a.astype(np.float64) @ w.astype(np.float64) + b
+    else:
+        gpu.matmul(gpu.upload(a), gpu.upload(w), c)
+        cpu = O.matmul(a, w)
+        exact = a.astype(np.float64) @ w.astype(np.float64)
+    got = gpu.download(c)
+    assert O.erro_rel(got, cpu) < 1e-4
+    assert_near_exact(got, exact, cpu, what=f"narrow {m}x{n}x{k}")
