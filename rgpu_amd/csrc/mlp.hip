@@ -45,7 +45,11 @@ struct Layer {
   size_t w_off = 0, b_off = 0;  // offsets (floats) into the flat parameter vectors
   void* act = nullptr;          // [batch, dout], f32 (or bf16 for mixed-precision hidden layers)
   float* delta = nullptr;       // [batch, dout] f32
-  void* delta_h = nullptr;      // [batch, dout] bf16 (mixed precision)
+  void* delta_h = nullptr;      // [batch, ldh] bf16 (mixed precision)
+  // Row stride of delta_h: dout, except for an output layer whose width is
+  // not a multiple of 64, padded so that its dX GEMM (K = its width) runs on
+  // whole 64-k stages; the padding columns stay zero.
+  size_t ldh = 0;
   int splits_dw = 1;
   int splits_fwd = 1;
   int splits_dx = 1;  // dX = δ·Wᵀ of this layer (l > 0)
@@ -57,6 +61,17 @@ struct Layer {
 };
 
 size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// K slices for a bf16 GEMM whose 256x256 tiles alone leave CUs idle: up to
+// 256 workgroups, at least 8 stages of 64 k per slice, and every slice whole
+// stages (so the direct-to-LDS kernel takes it).
+int half_slices(size_t m, size_t n, size_t k) {
+  const size_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  if (tiles >= 256 || k % 64 != 0) return 1;
+  int s = (int)std::min<size_t>(256 / tiles, k / 512);
+  while (s > 1 && k % (64 * (size_t)s) != 0) --s;
+  return std::max(s, 1);
+}
 
 }  // namespace
 
@@ -207,7 +222,7 @@ static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float s
     Layer& top = p->L[nl - 1];
     Launch Lz(c, "softmax_xent");
     hipError_t e = xent_launch(c->stream, (const float*)top.act, (const uint32_t*)labels->ptr, top.delta, top.delta_h,
-                               p->loss_rows, B, (int)top.dout, scale / (float)B, c->d_flags);
+                               p->loss_rows, B, (int)top.dout, scale / (float)B, c->d_flags, (int)top.ldh);
     if (e != hipSuccess) return hip_fail(c, e, "softmax_xent");
   }
   return RT_OK;
@@ -351,10 +366,17 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     // batches, the hidden layers' forward and dX too, whose bias+ReLU or
     // ReLU-mask epilogue then runs in the reduction (f32 plans; the bf16
     // plan's hidden outputs are bf16, which the reduction does not write).
-    const bool small_ok = last || !p->mixed;
-    Ly.splits_fwd = small_ok ? (int)rt_splitk_slices(batch, Ly.dout, Ly.din) : 1;
-    Ly.splits_dx = (l > 0 && !p->mixed) ? (int)rt_splitk_slices(batch, Ly.din, Ly.dout) : 1;
-    Ly.splits_dw = (int)rt_splitk_slices(Ly.din, Ly.dout, batch);
+    // The bf16 plan counts its 256x256 tiles instead (half_slices): a
+    // 1000-class head at batch 4096 has 64 of them.
+    if (p->mixed) {
+      Ly.splits_fwd = last ? half_slices(batch, Ly.dout, Ly.din) : 1;
+      Ly.splits_dw = half_slices(Ly.din, Ly.dout, batch);
+    } else {
+      Ly.splits_fwd = (int)rt_splitk_slices(batch, Ly.dout, Ly.din);
+      Ly.splits_dx = l > 0 ? (int)rt_splitk_slices(batch, Ly.din, Ly.dout) : 1;
+      Ly.splits_dw = (int)rt_splitk_slices(Ly.din, Ly.dout, batch);
+    }
+    Ly.ldh = (p->mixed && last) ? round_up(Ly.dout, 64) : Ly.dout;
     Ly.lbl_fwd = "fwd_l" + std::to_string(l);
     Ly.lbl_fwd_red = "fwd_reduce_l" + std::to_string(l);
     Ly.lbl_dw = "dw_l" + std::to_string(l);
@@ -405,7 +427,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     size_t elems = batch * p->L[l].dout;
     o_act[l] = reserve(elems * ((p->mixed && !last) ? 2 : 4));
     o_delta[l] = reserve(elems * 4);
-    o_delta_h[l] = p->mixed ? reserve(elems * 2) : 0;
+    o_delta_h[l] = p->mixed ? reserve(batch * p->L[l].ldh * 2) : 0;
   }
   size_t o_part = reserve(part * 4);
   std::vector<size_t> o_dw_part(n_layers, 0);
@@ -481,7 +503,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
       const Layer& Ly = p->L[l];
       const void* a_in = l == 0 ? nullptr : p->L[l - 1].act;
       const GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, a_in, Ly.delta_h, p->grad + Ly.w_off, RT_F32, (int)Ly.din,
-                                    (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr,
+                                    (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.ldh, RT_EPI_NONE, nullptr, nullptr,
                                     RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
       n += gemm_launch_count(dw) - 1;
     }
@@ -495,7 +517,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     for (int l = 0; l < n_layers; ++l) {
       const Layer& Ly = p->L[l];
       GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, l == 0 ? nullptr : p->L[l - 1].act, Ly.delta_h, p->grad + Ly.w_off,
-                              RT_F32, (int)Ly.din, (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.dout, RT_EPI_NONE,
+                              RT_F32, (int)Ly.din, (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.ldh, RT_EPI_NONE,
                               nullptr, nullptr, RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
       dw.nf_flag = p->state + 1;
       unchecked += !gemm_checks_nonfinite(dw);
@@ -553,9 +575,10 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     Layer& Ly = p->L[l];
     const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
     const void* dl = p->mixed ? Ly.delta_h : (const void*)Ly.delta;
+    const int ld_dl = (int)Ly.ldh;  // == dout for f32 plans and hidden layers
     // dW_l = A_{l-1}ᵀ·δ_l  (TN; A stored [batch, din]), db_l = 1ᵀ·δ_l fused.
     GemmDesc dw = plan_desc(p, RT_TN, in_dtype, in, dl, p->grad + Ly.w_off, RT_F32, (int)Ly.din, (int)Ly.dout, B,
-                            (int)Ly.din, (int)Ly.dout, RT_EPI_NONE, nullptr, nullptr, RT_F32, p->grad + Ly.b_off,
+                            (int)Ly.din, ld_dl, RT_EPI_NONE, nullptr, nullptr, RT_F32, p->grad + Ly.b_off,
                             Ly.splits_dw, Ly.dw_parts);
     if (p->mixed) {
       // The overflow flag is set by the GEMM's own epilogue where it can;
@@ -574,9 +597,11 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       Layer& Lp = p->L[l - 1];
       const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
       // δ_{l-1} = (δ_l·W_lᵀ) ⊙ 1[A_{l-1} > 0]  (NT; W stored [din, dout] = [N, K]).
+      // With a padded δ_l (ld_dl > dout) K runs over the zero padding too:
+      // those k read W's next row (finite weights) times zero.
       void* dst = p->mixed ? Lp.delta_h : (void*)Lp.delta;
       const GemmDesc dx = plan_desc(p, RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B, (int)Ly.din,
-                                    (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
+                                    ld_dl, ld_dl, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
                                     p->mixed ? RT_BF16 : RT_F32, nullptr, Ly.splits_dx);
       if (Ly.pair_bwd) {
         // Both read δ_l and neither feeds the other: one launch.

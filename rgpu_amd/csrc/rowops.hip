@@ -35,11 +35,12 @@ __device__ inline float bf16_to_f32(unsigned short h) { return __uint_as_float((
 
 // One wave per row: max, Σexp, p = e/Σ, δ = (p − onehot)·scale, loss = −ln max(p_y, 1e-12).
 // A label >= cols raises err_flag (plain store) and makes that row's loss NaN;
-// nothing is read out of bounds.
+// nothing is read out of bounds.  The optional bf16 copy of δ has row stride
+// ld_half (>= cols; its columns past cols are left alone).
 __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ logits, const uint32_t* __restrict__ labels,
                                                    float* __restrict__ delta, unsigned short* __restrict__ delta_bf16,
-                                                   float* __restrict__ loss_rows, int rows, int cols, float scale,
-                                                   int* err_flag) {
+                                                   int ld_half, float* __restrict__ loss_rows, int rows, int cols,
+                                                   float scale, int* err_flag) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
     const float yj = (!bad && (uint32_t)j == y) ? 1.0f : 0.0f;
     const float dj = (pj - yj) * scale;
     d[j] = dj;
-    if (delta_bf16 != nullptr) delta_bf16[(long long)row * cols + j] = f32_to_bf16_rne(dj);
+    if (delta_bf16 != nullptr) delta_bf16[(long long)row * ld_half + j] = f32_to_bf16_rne(dj);
     if (!bad && (uint32_t)j == y) loss_rows[row] = -logf(fmaxf(pj, 1e-12f));
   }
 }
@@ -284,10 +285,11 @@ hipError_t argmax_launch(hipStream_t s, const float* z, uint32_t* out, int rows,
 }
 
 hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* labels, float* delta, void* delta_half,
-                       float* loss_rows, int rows, int cols, float scale, int* err_flag) {
+                       float* loss_rows, int rows, int cols, float scale, int* err_flag, int ld_half) {
   if (rows <= 0) return hipSuccess;
+  if (ld_half < cols) ld_half = cols;
   hipLaunchKernelGGL(xent_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, logits, labels, delta,
-                     static_cast<unsigned short*>(delta_half), loss_rows, rows, cols, scale, err_flag);
+                     static_cast<unsigned short*>(delta_half), ld_half, loss_rows, rows, cols, scale, err_flag);
   return hipGetLastError();
 }
 

@@ -160,8 +160,9 @@ size_t colsum_scratch_elems(int rows, int cols);
 hipError_t bias_add_launch(hipStream_t s, float* z, const float* b, int rows, int cols);
 hipError_t relu_launch(hipStream_t s, const float* x, float* y, size_t n);
 hipError_t relu_bwd_launch(hipStream_t s, const void* a, int a_dtype, float* delta, size_t n);
+// delta_half (optional bf16 copy of δ) has row stride ld_half (0: cols).
 hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* labels, float* delta, void* delta_half,
-                       float* loss_rows, int rows, int cols, float scale, int* err_flag);
+                       float* loss_rows, int rows, int cols, float scale, int* err_flag, int ld_half = 0);
 // Output layer z = A·W + b (f32, cols <= 16 classes, K a multiple of 128, A
 // 16-byte aligned) fused with
 // the softmax cross-entropy of xent_launch; labels == nullptr writes only z.
