@@ -223,3 +223,36 @@ def test_training_is_deterministic(gpu):
         outs.append(mlp.weights())
     for a, b in zip(*outs):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("case", ["gpu_rs_tiny", "gpu_rs_split_k", "config_b32_sgd"])
+def test_step_matches_committed_oracle_vectors(gpu, case):
+    """One GPU step on the cases of tests/golden/oracle_vectors.json against
+    the oracle outputs committed there (not recomputed): loss within 1e-4,
+    every sampled gradient element within erro_rel 1e-4, and for SGD the
+    updated weights too (an Adam step from identical weights moves near-zero
+    gradients by ±lr either way, so only its gradients are compared)."""
+    import json
+    import os
+    from tests.golden import make_oracle_vectors as mov
+
+    with open(os.path.join(os.path.dirname(mov.__file__), "oracle_vectors.json")) as f:
+        want = json.load(f)[case]
+    name, params, x, lab, opt, lr = next(c for c in mov.cases() if c[0] == case)
+    mlp = G.GpuMlp.from_params(gpu, params, x.shape[0], lr if opt != "none" else 0.0,
+                               optimizer="sgd" if opt == "sgd" else "adam")
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+
+    def f32(h):
+        return np.uint32(int(h, 16)).view(np.float32)
+
+    assert abs(mlp.last_loss() - f32(want["loss"])) < 1e-4
+    checks = [("grads", mlp.grads())] + ([("weights", mlp.weights())] if opt == "sgd" else [])
+    for key, got in checks:
+        for t, (g, w) in enumerate(zip(got, want[key])):
+            assert list(g.shape) == w["shape"]
+            idx = np.array([i for i, _ in w["samples"]])
+            ref = np.array([f32(h) for _, h in w["samples"]], np.float32)
+            e = O.erro_rel(g.reshape(-1)[idx], ref)
+            assert e <= 1e-4, (case, key, t, e)
+    mlp.destroy()

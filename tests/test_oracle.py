@@ -379,3 +379,19 @@ def test_cpu_mlp_step_matches_tape_composition():
     assert loss == l.item()
     for a, p in zip(cpu.grads(), [p for l_ in layers for p in l_.params()]):
         assert np.array_equal(a, t.grad(p))
+
+
+def test_oracle_reproduces_committed_mlp_vectors():
+    # tests/golden/oracle_vectors.json: the oracle's loss, gradients and
+    # updated weights on the three MLP cases the GPU tests use, bit for bit
+    # (SHA-256 of every tensor); a change to the oracle's arithmetic shows here.
+    import json
+    import os
+    from tests.golden import make_oracle_vectors as mov
+
+    with open(os.path.join(os.path.dirname(mov.__file__), "oracle_vectors.json")) as f:
+        want = json.load(f)
+    got = mov.build()
+    assert got.keys() == want.keys()
+    for name in want:
+        assert got[name] == want[name], name
