@@ -30,6 +30,7 @@ no gfx950 device is present, construction fails loudly.
 from __future__ import annotations
 
 import ctypes as C
+import math
 import os
 from typing import List, Optional, Sequence
 
@@ -158,6 +159,16 @@ def _np_dtype(dt: int):
     return {F32: np.float32, BF16: np.uint16, F16: np.float16, U32: np.uint32}[dt]
 
 
+_ITEMSIZE = {F32: 4, BF16: 2, F16: 2, U32: 4}
+
+
+def _shape(shape) -> tuple:
+    """A shape as a tuple of Python ints (the common case passes through)."""
+    if type(shape) is tuple and all(type(d) is int for d in shape):
+        return shape
+    return tuple(int(d) for d in shape)
+
+
 def f32_to_bf16_bits(a) -> np.ndarray:
     """Round-to-nearest-even f32 -> bf16, returned as uint16 bit patterns."""
     u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
@@ -177,18 +188,18 @@ class GpuTensor:
     def __init__(self, gpu: "Gpu", handle: int, shape, dtype: int):
         self.gpu = gpu
         self.handle = handle
-        self.shape = tuple(int(s) for s in shape)
+        self.shape = _shape(shape)
         self.dtype = dtype
 
     def __len__(self):
-        return int(np.prod(self.shape)) if self.shape else 1
+        return math.prod(self.shape)
 
     @property
     def len(self) -> int:
         return len(self)
 
     def free(self):
-        if self.handle and self.gpu._h:
+        if self.handle and self.gpu._h and not self.gpu._keep(self):
             self.gpu._call("rt_free", self.gpu._h, self.handle)
         self.handle = None
 
@@ -209,9 +220,28 @@ class Gpu:
         if rc != 0:
             raise RtError(rc, L.rt_last_error(None).decode())
         self._h = h.value
+        # Freed buffers kept for the next ``empty`` of the same shape and dtype
+        # (an op-level tape allocates and drops the same shapes every step):
+        # no call into the library either way.  Reuse is safe for the same
+        # reason as the library's own cache: the context's work runs in order
+        # on its one stream.
+        self._spare = {}
+
+    _SPARE_PER_SHAPE = 8
+    _SPARE_MAX_BYTES = 64 << 20
+
+    def _keep(self, t: "GpuTensor") -> bool:
+        if len(t) * _ITEMSIZE[t.dtype] > self._SPARE_MAX_BYTES:
+            return False
+        lst = self._spare.setdefault((t.shape, t.dtype), [])
+        if len(lst) >= self._SPARE_PER_SHAPE:
+            return False
+        lst.append(t.handle)
+        return True
 
     def close(self):
         if self._h:
+            self._spare = {}  # the context frees every buffer it still owns
             lib().rt_close(self._h)
             self._h = None
 
@@ -238,7 +268,7 @@ class Gpu:
 
     # --------------------------------------------------------------- buffers
     def zeros(self, shape, dtype: int = F32) -> GpuTensor:
-        shape = tuple(int(s) for s in shape)
+        shape = _shape(shape)
         arr = (C.c_size_t * max(len(shape), 1))(*shape)
         h = C.c_void_p()
         self._call("rt_zeros", self._h, dtype, arr, len(shape), C.byref(h))
@@ -246,7 +276,10 @@ class Gpu:
 
     def empty(self, shape, dtype: int = F32) -> GpuTensor:
         """A buffer whose contents are undefined, for outputs written whole."""
-        shape = tuple(int(s) for s in shape)
+        shape = _shape(shape)
+        lst = self._spare.get((shape, dtype))
+        if lst:
+            return GpuTensor(self, lst.pop(), shape, dtype)
         arr = (C.c_size_t * max(len(shape), 1))(*shape)
         h = C.c_void_p()
         self._call("rt_empty", self._h, dtype, arr, len(shape), C.byref(h))
