@@ -45,12 +45,6 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const float* z = logits + (long long)row * cols;
-  float mx = -INFINITY;
-  for (int j = lane; j < cols; j += 64) mx = fmaxf(mx, z[j]);
-  mx = wave_max(mx);
-  float sum = 0.0f;
-  for (int j = lane; j < cols; j += 64) sum += expf(z[j] - mx);
-  sum = wave_sum(sum);
   const uint32_t y = labels[row];
   const bool bad = y >= (uint32_t)cols;
   if (bad && lane == 0) {
@@ -58,14 +52,44 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
     loss_rows[row] = __uint_as_float(0x7fc00000u);
   }
   float* d = delta + (long long)row * cols;
-  for (int j = lane; j < cols; j += 64) {
-    const float pj = expf(z[j] - mx) / sum;
+  auto put = [&](int j, float pj) {
     const float yj = (!bad && (uint32_t)j == y) ? 1.0f : 0.0f;
     const float dj = (pj - yj) * scale;
     d[j] = dj;
     if (delta_bf16 != nullptr) delta_bf16[(long long)row * ld_half + j] = f32_to_bf16_rne(dj);
     if (!bad && (uint32_t)j == y) loss_rows[row] = -logf(fmaxf(pj, 1e-12f));
+  };
+  constexpr int R = 16;  // row values per lane held in registers (rows up to 1024)
+  if (cols <= 64 * R) {
+    // One read of the row; the same operations in the same order as below.
+    float v[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) v[q] = z[min(lane + 64 * q, cols - 1)];  // all issued at once, in bounds
+    float mx = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+      if (lane + 64 * q < cols) mx = fmaxf(mx, v[q]);
+    mx = wave_max(mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+      if (lane + 64 * q < cols) {
+        v[q] = expf(v[q] - mx);
+        sum += v[q];
+      }
+    sum = wave_sum(sum);
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+      if (lane + 64 * q < cols) put(lane + 64 * q, v[q] / sum);
+    return;
   }
+  float mx = -INFINITY;
+  for (int j = lane; j < cols; j += 64) mx = fmaxf(mx, z[j]);
+  mx = wave_max(mx);
+  float sum = 0.0f;
+  for (int j = lane; j < cols; j += 64) sum += expf(z[j] - mx);
+  sum = wave_sum(sum);
+  for (int j = lane; j < cols; j += 64) put(j, expf(z[j] - mx) / sum);
 }
 
 // Narrow output layer fused with the loss: z = A·W + b for C <= 16 classes
