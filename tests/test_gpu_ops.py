@@ -469,3 +469,37 @@ def test_narrow_f32_product(gpu, m, n, k, bias):
     got = gpu.download(c)
     assert O.erro_rel(got, cpu) < 1e-4
     assert_near_exact(got, exact, cpu, what=f"narrow {m}x{n}x{k}")
+
+
+def test_contexts_are_independent_and_usable_from_other_threads():
+    """Two contexts in one process keep their own streams, buffers and caches,
+    and a context opened on one thread works from another (every entry point
+    makes the context's device current first)."""
+    import threading
+
+    r = np.random.default_rng(31)
+    a, b = r.standard_normal((130, 70)).astype(np.float32), r.standard_normal((70, 90)).astype(np.float32)
+    want = O.matmul(a, b)
+    g1, g2 = G.Gpu(0), G.Gpu(0)
+    try:
+        c1 = g1.empty((130, 90))
+        c2 = g2.empty((130, 90))
+        g1.matmul(g1.upload(a), g1.upload(b), c1)
+        g2.matmul(g2.upload(a), g2.upload(b), c2)
+        out = {}
+
+        def worker():
+            c = g1.empty((130, 90))
+            g1.matmul(g1.upload(a), g1.upload(b), c)
+            out["c"] = g1.download(c)
+
+        t = threading.Thread(target=worker)
+        t.start()
+        t.join()
+        for got in (g1.download(c1), g2.download(c2), out["c"]):
+            assert O.erro_rel(got, want) < 1e-5
+        with pytest.raises(G.RtError):
+            g2._call("rt_free", g2._h, c1.handle)  # a buffer of the other context
+    finally:
+        g1.close()
+        g2.close()
