@@ -462,8 +462,8 @@ struct DmaOperand {
 // checks (the host only takes this path for whole, aligned tiles).
 template <int EPI, bool OUT_BF16, int TM, int TN>
 __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[TM][TN], int m0, int n0, int wm,
-                                             int wn, int g, int r) {
-  float* Cf = static_cast<float*>(p.C) + (gridDim.z > 1 ? (long long)blockIdx.z * p.split_stride : 0);
+                                             int wn, int g, int r, int slice) {
+  float* Cf = static_cast<float*>(p.C) + (gridDim.z > 1 ? (long long)slice * p.split_stride : 0);
   unsigned short* Ch = static_cast<unsigned short*>(p.C);
   int bad = 0;
 #pragma unroll
@@ -511,22 +511,22 @@ __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[
 
 template <int TM, int TN>
 __device__ __forceinline__ void store_direct_any(const HalfArgs& p, const f4 (&acc)[TM][TN], int m0, int n0, int wm,
-                                                 int wn, int g, int r) {
-  if (gridDim.z > 1) return store_direct<RT_EPI_NONE, false>(p, acc, m0, n0, wm, wn, g, r);  // raw partial plane
+                                                 int wn, int g, int r, int slice) {
+  if (gridDim.z > 1) return store_direct<RT_EPI_NONE, false>(p, acc, m0, n0, wm, wn, g, r, slice);  // raw partial plane
   const bool hb = p.out_bf16;
   switch (p.epi) {
     case RT_EPI_BIAS:
-      return hb ? store_direct<RT_EPI_BIAS, true>(p, acc, m0, n0, wm, wn, g, r)
-                : store_direct<RT_EPI_BIAS, false>(p, acc, m0, n0, wm, wn, g, r);
+      return hb ? store_direct<RT_EPI_BIAS, true>(p, acc, m0, n0, wm, wn, g, r, slice)
+                : store_direct<RT_EPI_BIAS, false>(p, acc, m0, n0, wm, wn, g, r, slice);
     case RT_EPI_BIAS_RELU:
-      return hb ? store_direct<RT_EPI_BIAS_RELU, true>(p, acc, m0, n0, wm, wn, g, r)
-                : store_direct<RT_EPI_BIAS_RELU, false>(p, acc, m0, n0, wm, wn, g, r);
+      return hb ? store_direct<RT_EPI_BIAS_RELU, true>(p, acc, m0, n0, wm, wn, g, r, slice)
+                : store_direct<RT_EPI_BIAS_RELU, false>(p, acc, m0, n0, wm, wn, g, r, slice);
     case RT_EPI_RELU_MASK:
-      return hb ? store_direct<RT_EPI_RELU_MASK, true>(p, acc, m0, n0, wm, wn, g, r)
-                : store_direct<RT_EPI_RELU_MASK, false>(p, acc, m0, n0, wm, wn, g, r);
+      return hb ? store_direct<RT_EPI_RELU_MASK, true>(p, acc, m0, n0, wm, wn, g, r, slice)
+                : store_direct<RT_EPI_RELU_MASK, false>(p, acc, m0, n0, wm, wn, g, r, slice);
     default:
-      return hb ? store_direct<RT_EPI_NONE, true>(p, acc, m0, n0, wm, wn, g, r)
-                : store_direct<RT_EPI_NONE, false>(p, acc, m0, n0, wm, wn, g, r);
+      return hb ? store_direct<RT_EPI_NONE, true>(p, acc, m0, n0, wm, wn, g, r, slice)
+                : store_direct<RT_EPI_NONE, false>(p, acc, m0, n0, wm, wn, g, r, slice);
   }
 }
 
@@ -559,9 +559,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
   const int g = lane >> 4, r = lane & 15;
   const int wm = (wave / WGN) * WM, wn = (wave % WGN) * WN;
 
-  int bid = blockIdx.x;
+  // Work item (K slice, tile) of this workgroup.  Consecutive workgroup ids
+  // go to the 8 XCDs in turn; when the grid divides by 8, each XCD takes a
+  // contiguous run of items instead (the tiles of one slice, then the next
+  // slice), so workgroups that read the same operand panels share an L2.
   const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  int bid = blockIdx.x, slice = blockIdx.z;
+  const int total = nb * (int)gridDim.z;
+  if ((total & 7) == 0) {
+    const int lin = blockIdx.x + nb * blockIdx.z;
+    const int w = (lin & 7) * (total >> 3) + (lin >> 3);
+    slice = w / nb;
+    bid = w - slice * nb;
+  }
   constexpr int GROUP = 8;
   const int per_group = GROUP * p.tiles_n;
   const int grp = bid / per_group;
@@ -572,7 +582,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
   const int tile_n = in_grp / gsize;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
 
-  const int kb = blockIdx.z * p.k_per_split;
+  const int kb = slice * p.k_per_split;
   const int nk = (min(p.K, kb + p.k_per_split) - kb) / BKD;  // whole stages (checked by the host)
 
   OpA oa;
@@ -709,8 +719,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
 #pragma unroll
     for (int e = 0; e < 8; ++e) red[kg * BN + 8 * c8 + e] = cs[e];
     __syncthreads();
-    float* dst = cs_shared ? p.cs_parts + ((long long)blockIdx.z * p.tiles_m + tile_m) * p.N
-                           : p.colsum + (long long)blockIdx.z * p.N;
+    float* dst = cs_shared ? p.cs_parts + ((long long)slice * p.tiles_m + tile_m) * p.N
+                           : p.colsum + (long long)slice * p.N;
     int bad = 0;
     for (int col = tid; col < BN && n0 + col < p.N; col += THREADS) {
       float v = 0.0f;
@@ -721,7 +731,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
     if (bad && p.nf_flag && !cs_shared) *p.nf_flag = 1;  // shares are checked once summed
   }
 
-  store_direct_any<TM, TN>(p, acc, m0, n0, wm, wn, g, r);
+  store_direct_any<TM, TN>(p, acc, m0, n0, wm, wn, g, r, slice);
 }
 
 // dst[z, n] = sum over t of parts[z * rows + t, n], t in increasing order:
