@@ -73,7 +73,7 @@ int ensure_scratch(rt_ctx* c, size_t elems);
 // context on another device.
 inline void bind_device(const rt_ctx* c) {
   int d = -1;
-  if (hipGetDevice(&d) != hipSuccess || d != c->device) hipSetDevice(c->device);
+  if (hipGetDevice(&d) != hipSuccess || d != c->device) (void)hipSetDevice(c->device);
 }
 
 #define CHECK_CTX(c)                           \

@@ -503,3 +503,38 @@ def test_contexts_are_independent_and_usable_from_other_threads():
     finally:
         g1.close()
         g2.close()
+
+
+@pytest.mark.parametrize("k,slices", [(4096, 64), (16384, 64), (65536, 32)])
+@pytest.mark.parametrize("dt", [G.F16, G.BF16])
+def test_half_split_k_streaming_shapes(gpu, k, slices, dt):
+    """Split-K half GEMMs with few 256x256 output tiles (512x512: 4 tiles)
+    and many slices (1 to 16 stages of 64 k per slice): NN and TN with the
+    bias gradient fused, against the oracle on the same rounded inputs, and
+    deterministic."""
+    m = n = 512
+    r = np.random.default_rng(k + slices)
+    a = r.standard_normal((k, m)).astype(np.float32) / np.float32(16.0)
+    b = r.standard_normal((k, n)).astype(np.float32) / np.float32(16.0)
+    if dt == G.F16:
+        ar, br = a.astype(np.float16).astype(np.float32), b.astype(np.float16).astype(np.float32)
+    else:
+        ar, br = G.bf16_bits_to_f32(G.f32_to_bf16_bits(a)), G.bf16_bits_to_f32(G.f32_to_bf16_bits(b))
+    want = O.matmul(O.transpose(ar), br)
+    exact = ar.T.astype(np.float64) @ br.astype(np.float64)
+    ga, gb = gpu.upload(a, dt), gpu.upload(b, dt)
+    part = gpu.zeros((slices * (m * n + n),))
+    c, cs = gpu.zeros((m, n)), gpu.zeros((1, n))
+    gpu.split_k(ga, gb, c, part, slices, True, colsum=cs)
+    got = gpu.download(c)
+    assert O.erro_rel(got, want) < 1e-4
+    assert_near_exact(got, exact, want, what=f"TN split {k}/{slices}")
+    assert O.erro_rel(gpu.download(cs), br.astype(np.float64).sum(0, keepdims=True)) < 1e-5
+    c2 = gpu.zeros((m, n))
+    gpu.split_k(ga, gb, c2, part, slices, True, colsum=cs)
+    assert np.array_equal(got, gpu.download(c2))
+    # NN: A stored [M, K]
+    gat = gpu.upload(np.ascontiguousarray(a.T), dt)
+    c3 = gpu.zeros((m, n))
+    gpu.split_k(gat, gb, c3, part, slices, False)
+    assert O.erro_rel(gpu.download(c3), want) < 1e-4
