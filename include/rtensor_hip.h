@@ -251,8 +251,11 @@ typedef enum {
   RT_LOSS_MAE = 1,                 /* losses.rs:46-53, on d = pred - target        */
   RT_LOSS_SOFTMAX_XENT = 2,        /* losses.rs:99-115, on p = softmax_rows(z)     */
   RT_LOSS_BCE = 3,                 /* losses.rs:143-162, on probabilities          */
-  RT_LOSS_SOFTMAX_XENT_LOGITS = 4  /* losses.rs:99-115 on the logits z: softmax,
+  RT_LOSS_SOFTMAX_XENT_LOGITS = 4, /* losses.rs:99-115 on the logits z: softmax,
                                       loss and dir in one pass per row            */
+  RT_LOSS_SOFTMAX_XENT_LOGITS_MEAN = 5 /* the same with dir = (P − Y)·(1/batch):
+                                      the VJP for ḡ = 1, as rt_fill_scaled(1,
+                                      batch, P − Y) gives it, bit for bit         */
 } rt_loss_kind;                    /* mse (losses.rs:31-34) is sub, square, mean    */
 
 /* Tensor::map (tensor.rs:160-181) with the forward closure of op:

@@ -41,8 +41,8 @@ from typing import Callable, Dict, List, Optional, Sequence, Tuple, Union
 
 import numpy as np
 
-from .gpu import (EPI_BIAS, EPI_BIAS_RELU, LOSS_BCE, LOSS_MAE, LOSS_SOFTMAX_XENT_LOGITS, NN, NT, TN, Gpu, GpuTensor,
-                  RtError, upload_labels)
+from .gpu import (EPI_BIAS, EPI_BIAS_RELU, LOSS_BCE, LOSS_MAE, LOSS_SOFTMAX_XENT_LOGITS,
+                  LOSS_SOFTMAX_XENT_LOGITS_MEAN, NN, NT, TN, Gpu, GpuTensor, RtError, upload_labels)
 
 Shape = Tuple[int, ...]
 
@@ -360,7 +360,7 @@ class Var:
                 acc = grads[p]
                 if acc is None:
                     grads[p] = gp
-                    shared[p] = gp is g
+                    shared[p] = gp is g or getattr(gp, "vjp_shared", False)
                 elif acc.shape == gp.shape and not shared[p]:
                     gpu.zip("add", acc, gp, acc)  # v̄_j += Jᵀ v̄_i in place
                 else:
@@ -435,11 +435,20 @@ def softmax_cross_entropy(logits: Var, targets) -> Var:
     y = _as_device(gpu, targets)
     if tuple(y.shape) != tuple(logits.shape):
         raise ValueError("logits and targets differ in shape")
-    value, dirn = gpu.empty(()), gpu.empty(logits.shape)
-    gpu.loss(LOSS_SOFTMAX_XENT_LOGITS, logits.value, y, value, dirn)  # softmax, loss and P − Y in one launch
+    # Softmax, loss and the gradient for ḡ = 1, (P − Y)·(1/n), in one launch:
+    # the VJP of a loss that is the root of backward() (its upstream is the
+    # seed of ones) is then that buffer, shared (never written through).
+    value, dmean = gpu.empty(()), gpu.empty(logits.shape)
+    gpu.loss(LOSS_SOFTMAX_XENT_LOGITS_MEAN, logits.value, y, value, dmean)
+    dmean.vjp_shared = True
     batch = float(np.float32(logits.shape[0]))
+    z = logits.value
 
     def bw(g):
+        if g is _ones(gpu, ()):
+            return dmean
+        dirn, scratch = gpu.empty(z.shape), gpu.empty(())
+        gpu.loss(LOSS_SOFTMAX_XENT_LOGITS, z, y, scratch, dirn)  # P − Y again
         dx = gpu.empty(dirn.shape)
         gpu.fill_scaled(g, dx, batch, dirn)
         return dx

@@ -229,8 +229,10 @@ hipError_t scalar_fill_launch(hipStream_t s, const float* scalar, float div, con
 hipError_t softmax_rows_launch(hipStream_t s, const float* z, float* y, long long rows, long long cols);
 hipError_t softmax_rows_vjp_launch(hipStream_t s, const float* sm, const float* g, float* dx, long long rows,
                                    long long cols);
+// dir = (P − Y)·dir_scale (1: the plain direction).
 hipError_t xent_logits_launch(hipStream_t s, const float* z, const float* y, float* dir, long long rows,
-                              long long cols, float div, float* out, float* scratch, size_t scratch_elems);
+                              long long cols, float div, float* out, float* scratch, size_t scratch_elems,
+                              float dir_scale);
 hipError_t loss_terms_launch(hipStream_t s, int kind, const float* p, const float* y, float* term, float* dir,
                              long long n);
 

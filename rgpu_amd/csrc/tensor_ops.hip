@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void loss_terms_kernel(int kind, const float* 
 __global__ __launch_bounds__(256) void xent_logits_kernel(const float* __restrict__ z, const float* __restrict__ y,
                                                           float* __restrict__ dir, long long rows, long long cols,
                                                           float* __restrict__ part, float div,
-                                                          float* __restrict__ out) {
+                                                          float* __restrict__ out, float dir_scale) {
   __shared__ float sh[256];
   const long long i = blockIdx.x * 256LL + threadIdx.x;
   float row_term = 0.0f;
@@ -291,7 +291,7 @@ __global__ __launch_bounds__(256) void xent_logits_kernel(const float* __restric
     for (long long j = 0; j < cols; ++j) {
       const float pj = d[j] / sum, yj = yr[j];
       if (yj != 0.0f) row_term += -(yj * logf(fmaxf(pj, 1e-12f)));
-      d[j] = pj - yj;
+      d[j] = (pj - yj) * dir_scale;  // dir_scale 1 leaves P − Y exactly as it is
     }
   }
   sh[threadIdx.x] = row_term;
@@ -449,11 +449,12 @@ hipError_t softmax_rows_vjp_launch(hipStream_t s, const float* sm, const float* 
 }
 
 hipError_t xent_logits_launch(hipStream_t s, const float* z, const float* y, float* dir, long long rows,
-                              long long cols, float div, float* out, float* scratch, size_t scratch_elems) {
+                              long long cols, float div, float* out, float* scratch, size_t scratch_elems,
+                              float dir_scale) {
   const long long blocks = std::max<long long>(1, (rows + 255) / 256);
   if (blocks > 1 && (size_t)blocks > scratch_elems) return hipErrorInvalidValue;
   hipLaunchKernelGGL(xent_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, z, y, dir, rows, cols, scratch, div,
-                     out);
+                     out, dir_scale);
   if (blocks > 1) hipLaunchKernelGGL(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)blocks, div, out);
   return hipGetLastError();
 }
@@ -659,7 +660,7 @@ int rt_loss(rt_ctx* c, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_b
   CHECK_CTX(c);
   if (!p || !value) return fail(c, RT_ERR_INVALID, "null buffer");
   if (kind != RT_LOSS_MAE && kind != RT_LOSS_SOFTMAX_XENT && kind != RT_LOSS_BCE &&
-      kind != RT_LOSS_SOFTMAX_XENT_LOGITS)
+      kind != RT_LOSS_SOFTMAX_XENT_LOGITS && kind != RT_LOSS_SOFTMAX_XENT_LOGITS_MEAN)
     return fail(c, RT_ERR_INVALID, "unknown loss kind %d", (int)kind);
   if (kind != RT_LOSS_MAE && !y) return fail(c, RT_ERR_INVALID, "this loss needs targets");
   if (!is_f32(p) || !is_f32(value) || (y && !is_f32(y)) || (dir && !is_f32(dir)))
@@ -668,7 +669,7 @@ int rt_loss(rt_ctx* c, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_b
   if (y && y->n != p->n) return fail(c, RT_ERR_SHAPE, "predictions and targets differ in size");
   if (dir && dir->n != p->n) return fail(c, RT_ERR_SHAPE, "dir must match the predictions");
   float batch = (float)p->n;
-  if (kind == RT_LOSS_SOFTMAX_XENT_LOGITS) {
+  if (kind == RT_LOSS_SOFTMAX_XENT_LOGITS || kind == RT_LOSS_SOFTMAX_XENT_LOGITS_MEAN) {
     if (p->rank != 2 || y->rank != 2 || y->shape[0] != p->shape[0] || y->shape[1] != p->shape[1])
       return fail(c, RT_ERR_SHAPE, "logits and targets differ in shape");  // losses.rs:100
     if (!dir) return fail(c, RT_ERR_INVALID, "the logits form writes dir (it holds the softmax on the way)");
@@ -680,7 +681,8 @@ int rt_loss(rt_ctx* c, rt_loss_kind kind, const rt_buf* p, const rt_buf* y, rt_b
     HIP_TRY(c,
             xent_logits_launch(c->stream, static_cast<const float*>(p->ptr), static_cast<const float*>(y->ptr),
                                static_cast<float*>(dir->ptr), rows, cols, (float)rows, static_cast<float*>(value->ptr),
-                               c->scratch, c->scratch_elems),
+                               c->scratch, c->scratch_elems,
+                               kind == RT_LOSS_SOFTMAX_XENT_LOGITS_MEAN ? 1.0f / (float)rows : 1.0f),
             "softmax-xent");
     return RT_OK;
   }

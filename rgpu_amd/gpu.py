@@ -48,7 +48,7 @@ PREC_F32, PREC_BF16 = 0, 1
 UNARY = {"scale": 0, "offset": 1, "neg": 2, "square": 3, "sqrt": 4, "exp": 5, "ln": 6, "relu": 7,
          "leaky_relu": 8, "sigmoid": 9, "tanh": 10}
 BINARY = {"add": 0, "sub": 1, "mul": 2, "div": 3}
-LOSS_MAE, LOSS_SOFTMAX_XENT, LOSS_BCE, LOSS_SOFTMAX_XENT_LOGITS = 1, 2, 3, 4
+LOSS_MAE, LOSS_SOFTMAX_XENT, LOSS_BCE, LOSS_SOFTMAX_XENT_LOGITS, LOSS_SOFTMAX_XENT_LOGITS_MEAN = 1, 2, 3, 4, 5
 
 STATUS = {0: "RT_OK", 1: "RT_ERR_NO_DEVICE", 2: "RT_ERR_INVALID", 3: "RT_ERR_SHAPE", 4: "RT_ERR_DTYPE",
           5: "RT_ERR_OOM", 6: "RT_ERR_LABEL", 7: "RT_ERR_HIP", 8: "RT_ERR_OVERFLOW"}

@@ -35,4 +35,5 @@ def test_op_tables_match_the_header():
     assert f"RT_LOSS_MAE = {G.LOSS_MAE}," in text
     assert f"RT_LOSS_SOFTMAX_XENT = {G.LOSS_SOFTMAX_XENT}," in text
     assert f"RT_LOSS_BCE = {G.LOSS_BCE}," in text
-    assert f"RT_LOSS_SOFTMAX_XENT_LOGITS = {G.LOSS_SOFTMAX_XENT_LOGITS} " in text
+    assert f"RT_LOSS_SOFTMAX_XENT_LOGITS = {G.LOSS_SOFTMAX_XENT_LOGITS}," in text
+    assert f"RT_LOSS_SOFTMAX_XENT_LOGITS_MEAN = {G.LOSS_SOFTMAX_XENT_LOGITS_MEAN} " in text

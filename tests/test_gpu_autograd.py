@@ -661,3 +661,24 @@ def test_xent_from_logits_matches_probability_form(gpu, rows, cols):
     assert bits_equal(gpu.download(d1), gpu.download(d2))
     a, b = float(gpu.download(v1)), float(gpu.download(v2))
     assert abs(a - b) <= 1e-6 * max(1.0, abs(a))
+
+
+def test_softmax_xent_gradient_off_the_root(gpu):
+    """The loss's VJP when its upstream is not the seed of ones (the loss is
+    scaled, or added to itself, before backward): P − Y recomputed and
+    scaled by ḡ / n, against the oracle's tape; the root case returns the
+    gradient computed in the forward launch, and a second backward pass over
+    the same tape gives the same bits (that buffer is never written through)."""
+    r = np.random.default_rng(77)
+    z = r.standard_normal((33, 7)).astype(np.float32)
+    y = A.one_hot(r.integers(0, 7, 33), 7)
+    for build in (lambda v: v.scale(3.0), lambda v: v.add(v), lambda v: v):
+        p = A.Param(gpu, "z", z)
+        total = build(A.softmax_cross_entropy(p.watch(A.Tape(gpu)), y))
+        g1 = gpu.download(total.backward().of(p))
+        g2 = gpu.download(total.backward().of(p))
+        assert bits_equal(g1, g2)
+        po = O.Param(z)
+        to = O.Tape()
+        build(O.loss("softmax_cross_entropy", to.watch(po), y)).backward()
+        assert O.erro_rel(g1, to.grad(po)) <= 1e-6
