@@ -95,11 +95,12 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
 // Narrow output layer fused with the loss: z = A·W + b for C <= 16 classes
 // (rtensor runs the head GEMM with split-K and then XENT, mod.rs:1360-1367 and
 // 1399-1410), then the softmax cross-entropy of xent_kernel, in one launch.
-// Block = 16 rows and 8 waves; wave w sums k in [w K/8, (w+1) K/8) with
-// v_mfma_f32_16x16x4_f32, both operands straight from global memory (A as
-// float4 row segments, W as scalars, 8 chunks of 16 k in flight per batch).
+// Block = 16 rows and HW waves (8, or 16 when K is a multiple of 256); wave w
+// sums k in [w K/HW, (w+1) K/HW) with v_mfma_f32_16x16x4_f32, both operands
+// straight from global memory (A as float4 row segments, W as scalars, 8
+// chunks of 16 k in flight per batch).
 // Lane (g, r) feeds A(row r, k) and W(k, class r) with k = chunk + 4g + s at
-// MFMA step s, and ends with z(rows 4g..4g+3, class r).  The eight partial
+// MFMA step s, and ends with z(rows 4g..4g+3, class r).  The HW partial
 // tiles are added in LDS in wave order; then the 16 lanes of each row run
 // the softmax with width-16 shuffles.  With labels == null only the logits
 // are written (and bias may be null: z = A·W).  The K sum order differs from the CPU path's; the rest
@@ -107,17 +108,18 @@ __global__ __launch_bounds__(256) void xent_kernel(const float* __restrict__ log
 typedef float f4v __attribute__((ext_vector_type(4)));
 constexpr int HEAD_C = 16, HEAD_ROWS = 16;
 
-__global__ __launch_bounds__(512) void head_xent_kernel(const float* __restrict__ A, int K,
-                                                        const float* __restrict__ W, const float* __restrict__ bias,
-                                                        const uint32_t* __restrict__ labels,
-                                                        float* __restrict__ logits, float* __restrict__ delta,
-                                                        float* __restrict__ loss_rows, int rows, int cols,
-                                                        float scale, int* err_flag) {
-  constexpr int HW = 8;  // waves
+template <int HW>  // waves per block: 8, or 16 when K is a multiple of 256
+__global__ __launch_bounds__(64 * HW) void head_xent_kernel(const float* __restrict__ A, int K,
+                                                            const float* __restrict__ W,
+                                                            const float* __restrict__ bias,
+                                                            const uint32_t* __restrict__ labels,
+                                                            float* __restrict__ logits, float* __restrict__ delta,
+                                                            float* __restrict__ loss_rows, int rows, int cols,
+                                                            float scale, int* err_flag) {
   __shared__ float red[HW][HEAD_ROWS][HEAD_C + 1];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, r = lane & 15;
   const int r0 = blockIdx.x * HEAD_ROWS;
-  const int kq = K / HW;       // k per wave (K is a multiple of 128)
+  const int kq = K / HW;       // k per wave (K is a multiple of 16 HW)
   const int nch = kq / 16;     // chunks of 16 k per wave
   const int kw = wave * kq;
   const float* arow = A + (long long)min(r0 + r, rows - 1) * K + kw + 4 * g;  // rows past the end read the last row
@@ -297,8 +299,14 @@ hipError_t head_xent_launch(hipStream_t s, const float* A, int K, const float* W
   if (!head_xent_supported(K, cols) || rows < 1 || (reinterpret_cast<uintptr_t>(A) & 15) != 0)
     return hipErrorInvalidValue;
   const unsigned blocks = (unsigned)((rows + HEAD_ROWS - 1) / HEAD_ROWS);
-  hipLaunchKernelGGL(head_xent_kernel, dim3(blocks), dim3(512), 0, s, A, K, W, bias, labels, logits, delta,
-                     loss_rows, rows, cols, scale, err_flag);
+  // 16 waves when K splits into 16 whole 16-k chunks per wave (shorter
+  // dependent load chains per wave; the block count is fixed by the rows).
+  if (K % 256 == 0)
+    hipLaunchKernelGGL(head_xent_kernel<16>, dim3(blocks), dim3(1024), 0, s, A, K, W, bias, labels, logits, delta,
+                       loss_rows, rows, cols, scale, err_flag);
+  else
+    hipLaunchKernelGGL(head_xent_kernel<8>, dim3(blocks), dim3(512), 0, s, A, K, W, bias, labels, logits, delta,
+                       loss_rows, rows, cols, scale, err_flag);
   return hipGetLastError();
 }
 
