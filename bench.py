@@ -120,7 +120,7 @@ def bench_step(gpu, G, steps, warmup):
     return wall, loss, prof, mlp.dispatches_por_passo()
 
 
-def bench_bwd_gemm(gpu, G, reps=10, rounds=5):
+def bench_bwd_gemm(gpu, G, reps=10, rounds=20):
     """Linear 4096->4096 backward at batch 8192, bf16 operands, f32 accumulate."""
     B, D = 8192, 4096
     rng = np.random.default_rng(3)
@@ -131,13 +131,15 @@ def bench_bwd_gemm(gpu, G, reps=10, rounds=5):
     dx = gpu.zeros((B, D), G.BF16)
     dw = gpu.zeros((D, D), G.F32)
     db = gpu.zeros((1, D), G.F32)
-    for _ in range(3):
+    # The device takes ~25 ms of this load to settle at its sustained clock
+    # (~1.95 GHz at the ~1.35 kW socket limit); the first rounds run up to
+    # 15% slower.  Warm up for ~80 ms before timing.
+    for _ in range(100):
         gpu.gemm(G.NT, gdy, gw, dx)
         gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
     gpu.sync()
     # Back-to-back launches between two HIP events on the library stream,
-    # dX and dW alternating in rounds (the sustained clock drifts as the
-    # device warms), median over the rounds.
+    # dX and dW alternating in rounds, median over the rounds.
     t_dx, t_dw = [], []
     for _ in range(rounds):
         gpu.timer_begin()
@@ -161,7 +163,7 @@ def bench_bwd_gemm(gpu, G, reps=10, rounds=5):
     }
 
 
-def bench_splitk(gpu, G, reps=10, slices=64):
+def bench_splitk(gpu, G, reps=50, slices=64):
     """Split-K weight gradient over a 262144-long batch, f16 operands."""
     K, M, N = 262144, 512, 512
     rng = np.random.default_rng(4)
@@ -169,7 +171,7 @@ def bench_splitk(gpu, G, reps=10, slices=64):
     dy = gpu.upload(rng.standard_normal((K, N), dtype=np.float32) / np.float32(16.0), G.F16)
     dw, db = gpu.zeros((M, N)), gpu.zeros((1, N))
     part = gpu.zeros((slices * (M * N + N),))
-    for _ in range(2):
+    for _ in range(200):  # ~40 ms: past the device's clock ramp
         gpu.split_k(x, dy, dw, part, slices, True, colsum=db)
     gpu.sync()
     gpu.timer_begin()
@@ -195,7 +197,7 @@ def bench_splitk(gpu, G, reps=10, slices=64):
             "frac": round(gbs / PEAK_HBM_GBS, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
 
 
-def bench_mixed(gpu, G, steps=20, warmup=3):
+def bench_mixed(gpu, G, steps=20, warmup=10):
     """8 x 4096 ReLU layers -> 1000 classes, batch 4096, bf16 + f32 master, Adam."""
     dims = [4096] * 9 + [1000]
     B = 4096
@@ -419,11 +421,14 @@ def cpu_baseline(budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy", "tape", "pcie"], default="all",
                     help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
+    ap.add_argument("--rounds", type=int, default=20,
+                    help="rounds of the bf16 backward pair for --only bwd (more rounds hold the load for "
+                         "power and clock sampling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the data-parallel "
@@ -436,7 +441,8 @@ def main():
     if args.only in ("bwd", "splitk", "mixed", "copy", "tape", "pcie"):
         fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed, "copy": bench_copy,
               "tape": bench_tape, "pcie": bench_pcie}[args.only]
-        print(json.dumps({args.only: fn(gpu, G)}), flush=True)
+        res = fn(gpu, G, rounds=args.rounds) if args.only == "bwd" else fn(gpu, G)
+        print(json.dumps({args.only: res}), flush=True)
         return
     wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
     ms = wall / args.steps * 1e3
