@@ -2,7 +2,7 @@
 
 This module wraps ``librtensor_cpu.so`` (built from ``rtensor_cpu.cpp`` by
 the Makefile beside it), a C++ restatement of rtensor's single-threaded CPU
-path.  It is the checker for the HIP backend in ``rgpu_amd`` and the CPU
+path.  It is the oracle the HIP backend in ``rgpu_amd`` is tested against, and the CPU
 baseline that ``bench.py`` times.  Only ``tests/``, ``__graft_entry__.smoke``
 and ``bench.py``'s ``cpu_baseline`` leg may import it; the product path never
 does.

@@ -8,8 +8,8 @@ from oracle import oracle as O
 
 
 def oracle_threads() -> int:
-    # Row-parallel oracle is bit-identical for any thread count; the GPU box
-    # gives a 16-CPU share.
+    # Row-parallel oracle is bit-identical for any thread count; at most 16
+    # threads, the CPU share of a one-GPU host.
     return max(1, min(16, os.cpu_count() or 1))
 
 
