@@ -1,6 +1,8 @@
 """The half-precision configurations the backend is measured on:
   * split-K weight gradient: dW = Xᵀ·dY with reduction length 262144, X and dY
     f16 ~N(0,1)/16 [262144, 512], f32 accumulate and output, db = colsum(dY);
+  * Linear 4096->4096 backward at batch 8192 in bf16: dX = dY·Wᵀ, dW = Xᵀ·dY,
+    db = colsum(dY), f32 accumulate;
   * the 8-layer 4096-wide ReLU MLP -> 1000 classes, batch 4096, bf16
     activations/weights with f32 master weights, static loss scale 1024 and
     fused Adam.
@@ -152,3 +154,45 @@ def test_mixed_precision_overflow_skips_update(gpu, dims, batch):
     mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, uniform_labels(2, batch, dims[-1])))
     assert not mlp.overflow()
     assert any(not np.array_equal(a, b) for a, b in zip(w0, mlp.weights()))
+
+
+def test_linear4096_backward_bf16_full_size(gpu):
+    """Linear 4096->4096 backward at batch 8192 (nn.rs:82-98 adjoints): X, dY
+    ~N(0,1)/64 and Kaiming-uniform W in bf16; dX = dY·Wᵀ (bf16 out), dW = Xᵀ·dY
+    (f32 out) with db = colsum(dY) fused.  db is checked whole, dX and dW on
+    256 sampled entries each against float64 dot products."""
+    B, D = 8192, 4096
+    rng = np.random.default_rng(33)
+    x32 = rng.standard_normal((B, D), dtype=np.float32) / np.float32(64)
+    dy32 = rng.standard_normal((B, D), dtype=np.float32) / np.float32(64)
+    lim = np.sqrt(6.0 / D)
+    w32 = rng.uniform(-lim, lim, size=(D, D)).astype(np.float32)
+    gx, gdy, gw = gpu.upload(x32, G.BF16), gpu.upload(dy32, G.BF16), gpu.upload(w32, G.BF16)
+    dx, dw, db = gpu.zeros((B, D), G.BF16), gpu.zeros((D, D)), gpu.zeros((1, D))
+    print(f"NT {B}x{D}x{D} then TN {D}x{D}x{B} with db", flush=True)
+    gpu.gemm(G.NT, gdy, gw, dx)
+    gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
+    got_dx, got_dw, got_db = gpu.download_f32(dx), gpu.download(dw), gpu.download(db)
+    x, dy, w = bf16_round(x32), bf16_round(dy32), bf16_round(w32)
+    # db whole, against the exact column sums of the rounded dY; f32
+    # accumulation stays far inside 1e-5 of the sum of magnitudes.
+    ex_b = dy.sum(0, keepdims=True, dtype=np.float64)
+    ab_b = np.abs(dy).sum(0, keepdims=True, dtype=np.float64)
+    assert np.all(np.abs(got_db - ex_b) <= 1e-5 * ab_b)
+    i, j = rng.integers(0, B, 256), rng.integers(0, D, 256)  # dX entries
+    p, q = rng.integers(0, D, 256), rng.integers(0, D, 256)  # dW entries
+    a_dx, b_dx = dy[i].astype(np.float64), w[j].astype(np.float64)
+    a_dw, b_dw = x[:, p].astype(np.float64), dy[:, q].astype(np.float64)
+    ex_dx, ab_dx = (a_dx * b_dx).sum(1), np.abs(a_dx * b_dx).sum(1)
+    ex_dw, ab_dw = (a_dw * b_dw).sum(0), np.abs(a_dw * b_dw).sum(0)
+    g_dx, g_dw = got_dx[i, j].astype(np.float64), got_dw[p, q].astype(np.float64)
+    # Same rounded operands: f32 accumulation, plus one bf16 rounding of dX.
+    assert np.all(np.abs(g_dw - ex_dw) <= 1e-5 * ab_dw)
+    assert np.all(np.abs(g_dx - ex_dx) <= 2.0 ** -8 * np.abs(ex_dx) + 1e-5 * ab_dx)
+    # Against the f32 inputs before rounding: within 2e-2.
+    f_dx = (dy32[i].astype(np.float64) * w32[j].astype(np.float64)).sum(1)
+    f_dw = (x32[:, p].astype(np.float64) * dy32[:, q].astype(np.float64)).sum(0)
+    e_dx = np.max(np.abs(g_dx - f_dx)) / np.max(np.abs(f_dx))
+    e_dw = np.max(np.abs(g_dw - f_dw)) / np.max(np.abs(f_dw))
+    print(f"vs f32 inputs: dX {e_dx:.2e}, dW {e_dw:.2e}", flush=True)
+    assert e_dx <= 2e-2 and e_dw <= 2e-2
