@@ -27,6 +27,14 @@ softmax_rows (455-472)       rows sum to 1, finite at logits 100 (autodiff.rs:62
 argmax_rows (476-493)        first-max tie rule on hand-built rows
 tape + VJPs (tape.rs, ops.rs) central-difference gradient checks of autodiff.rs:81-173;
                              fan-out accumulation KAT [3,5,7] (autodiff.rs:175-184)
+div VJP (ops.rs:93-102)      float64 closed form (A/B: g/B, -g·A/B²) over 5 broadcast
+                             shape pairs incl. reduction axes; central differences
+offset, sqrt, exp VJPs       float64 derivative (1, 1/(2√x), eˣ) times a random
+(ops.rs:139-142, 158-170)    upstream, within 1e-6; central differences of the forward
+leaky_relu VJP (197-203)     float64 derivative; x = ±0 takes the slope; the slope
+                             argument is honoured (two slopes, exact)
+mae (losses.rs:46-53)        value vs float64; gradient exactly sign(d)·(ḡ/N) with
+                             sign(0) = +1 and ḡ = 3; central differences off the kink
 softmax_cross_entropy        numeric gradient check; delta rows sum to 0;
 (losses.rs:99-115)           delta[r, y_r] in [-1/B, 0]; loss = mean(-ln p_y) in float64
 Sgd (optim.rs:80-114)        exact axpy; momentum convergence (autodiff.rs:214-231)

@@ -253,6 +253,119 @@ def test_explicit_softmax_ln_gradient_matches_numeric():  # autodiff.rs:150-173
     _numeric_check(model.params(), g, loss_fn)
 
 
+def _upstream_vjp(op, x, w, k=0.0):
+    """x̄ of sum(w ⊙ op(x)) through the tape: the op's VJP applied to the
+    upstream gradient w (mul and sum are pinned above)."""
+    t = O.Tape()
+    p = O.Param(x)
+    y = getattr(t.watch(p), op)(k)
+    y.mul(t.constant(w)).sum().backward()
+    return y.value(), t.grad(p)
+
+
+def _forward(op, x, k=0.0):
+    return getattr(O.Tape().constant(x), op)(k).value().astype(np.float64)
+
+
+# Each case: x, the float64 derivative, the tolerance of the closed-form check.
+# ops.rs:139-142 (offset), 158-162 (sqrt), 166-170 (exp), 197-203 (leaky_relu).
+_ELEMENTWISE = {
+    "offset": (lambda r: r.uniform(-3, 3, (4, 6)), lambda x, k: np.ones_like(x), 2.5),
+    "sqrt": (lambda r: r.uniform(0.05, 4.0, (4, 6)), lambda x, k: 0.5 / np.sqrt(x), 0.0),
+    "exp": (lambda r: r.uniform(-3, 3, (4, 6)), lambda x, k: np.exp(x), 0.0),
+    "leaky_relu": (lambda r: r.uniform(-3, 3, (4, 6)), lambda x, k: np.where(x > 0, 1.0, k), 0.1),
+}
+
+
+@pytest.mark.parametrize("op", sorted(_ELEMENTWISE))
+def test_elementwise_vjp_matches_float64_derivative_and_numeric(op):
+    make_x, deriv, k = _ELEMENTWISE[op]
+    rng = np.random.default_rng(41)
+    x = make_x(rng).astype(np.float32)
+    w = rng.normal(size=x.shape).astype(np.float32)  # a non-uniform upstream gradient
+    _, got = _upstream_vjp(op, x, w, k)
+    want = w.astype(np.float64) * deriv(x.astype(np.float64), np.float64(np.float32(k)))
+    # closed form: the f32 VJP rounds a few times (g/(2y), g·y)
+    assert np.all(np.abs(got - want) <= 1e-6 * np.abs(want) + 1e-30), (got, want)
+    # central differences of the oracle's own forward (autodiff.rs:6-37 method);
+    # elementwise, so all entries at once
+    h = 1e-3
+    num = (_forward(op, x + np.float32(h), k) - _forward(op, x - np.float32(h), k)) / (
+        (x + np.float32(h)).astype(np.float64) - (x - np.float32(h)).astype(np.float64))
+    num *= w
+    assert np.all(np.abs(num - got) <= 2e-3 * (1 + np.maximum(np.abs(num), np.abs(got)))), (num, got)
+
+
+def test_leaky_relu_vjp_at_zero_and_slope_argument():
+    # 1[X > 0] + s·1[X ≤ 0]: x = 0 takes the slope, and k is the slope
+    x = np.array([[0.0, -0.0, 1e-30, -1e-30, 2.0, -2.0]], np.float32)
+    w = np.array([[1.0, 2.0, 3.0, 4.0, 5.0, 6.0]], np.float32)
+    for s in (0.01, 0.3):
+        y, g = _upstream_vjp("leaky_relu", x, w, s)
+        sf = np.float32(s)
+        assert g.reshape(-1).tolist() == [sf * 1, sf * 2, 3.0, np.float32(sf * 4), 5.0, np.float32(sf * 6)]
+        assert y.reshape(-1).tolist() == [0.0, 0.0, np.float32(1e-30), np.float32(sf * np.float32(-1e-30)),
+                                          2.0, np.float32(sf * -2)]
+
+
+@pytest.mark.parametrize("sa,sb", [((3, 5), (3, 5)), ((3, 5), (1, 5)), ((3, 5), (3, 1)),
+                                   ((1, 5), (3, 5)), ((3, 1), (1, 5))])
+def test_div_vjp_matches_float64_and_numeric(sa, sb):  # ops.rs:93-102
+    rng = np.random.default_rng(43)
+    a = rng.uniform(-2, 2, sa).astype(np.float32)
+    b = (rng.uniform(0.5, 2.0, sb) * rng.choice([-1.0, 1.0], sb)).astype(np.float32)
+    out_shape = np.broadcast_shapes(sa, sb)
+    w = rng.normal(size=out_shape).astype(np.float32)
+    pa, pb = O.Param(a), O.Param(b)
+
+    def build(t):
+        return t.watch(pa).div(t.watch(pb)).mul(t.constant(w)).sum()
+
+    t = O.Tape()
+    build(t).backward()
+    ga, gb = t.grad(pa), t.grad(pb)
+    a64, b64, w64 = a.astype(np.float64), b.astype(np.float64), w.astype(np.float64)
+    want_a = np.broadcast_to(w64 / b64, out_shape)
+    want_b = np.broadcast_to(-w64 * a64 / (b64 * b64), out_shape)
+    want_a = want_a.sum(axis=tuple(i for i in range(2) if sa[i] == 1), keepdims=True)
+    want_b = want_b.sum(axis=tuple(i for i in range(2) if sb[i] == 1), keepdims=True)
+    assert ga.shape == sa and gb.shape == sb
+    assert np.allclose(ga, want_a, rtol=1e-5, atol=1e-6)
+    assert np.allclose(gb, want_b, rtol=1e-5, atol=1e-6)
+    _numeric_check([pa, pb], [ga, gb], lambda: build(O.Tape()).item(), h=1e-2)
+
+
+def test_mae_gradient_closed_form_subgradient_and_upstream():  # losses.rs:46-53
+    rng = np.random.default_rng(47)
+    pred = rng.normal(size=(4, 3)).astype(np.float32)
+    target = rng.normal(size=(4, 3)).astype(np.float32)
+    target[0, 1], target[2, 2] = pred[0, 1], pred[2, 2]  # ties take sign(0) = +1
+    p = O.Param(pred)
+    t = O.Tape()
+    l = O.loss("mae", t.watch(p), target)
+    # the upstream ḡ = 3 reaches the gradient through ḡ/N
+    l.scale(3.0).backward()
+    d = pred.astype(np.float64) - target.astype(np.float64)
+    assert abs(l.item() - np.abs(d).mean()) < 1e-6
+    sign = np.where(d >= 0, 1.0, -1.0)
+    assert np.array_equal(t.grad(p), (sign * (np.float32(3.0) / np.float32(12))).astype(np.float32))
+    # numeric on the entries away from the kink
+    t2 = O.Tape()
+    O.loss("mae", t2.watch(p), target).backward()
+    g = t2.grad(p)
+    h = 1e-3
+    for i in range(pred.size):
+        if abs(d.reshape(-1)[i]) < 10 * h:
+            continue
+        up, dn = pred.copy().reshape(-1), pred.copy().reshape(-1)
+        up[i] += np.float32(h)
+        dn[i] -= np.float32(h)
+        lu = O.loss("mae", O.Tape().constant(up.reshape(pred.shape)), target).item()
+        ld = O.loss("mae", O.Tape().constant(dn.reshape(pred.shape)), target).item()
+        num = (lu - ld) / (float(up[i]) - float(dn[i]))
+        assert abs(num - g.reshape(-1)[i]) < 1e-3 * (1 + abs(num)), (i, num, g.reshape(-1)[i])
+
+
 def test_fan_out_accumulates():  # autodiff.rs:175-184
     w = O.Param(np.array([[1.0, 2.0, 3.0]], np.float32))
     t = O.Tape()
