@@ -185,20 +185,38 @@ int rt_mlp_create(rt_ctx* ctx, int n_layers, const size_t* dims, const float* co
 int rt_mlp_destroy(rt_mlp* mlp);
 /* GpuMlp::step (mod.rs:1499-1511): forward, softmax cross-entropy, backward
  * and optimizer update, enqueued without waiting.  x is [batch, dims[0]]
- * (f32, or bf16 for RT_PREC_BF16), labels u32 [batch]. */
+ * (f32, or bf16 for RT_PREC_BF16), labels u32 [batch].  A label >= the
+ * number of classes (undefined behaviour in the reference's XENT,
+ * kernels.rs:158-159) raises the plan's own label flag: that update and every
+ * later one are skipped (weights, moments and t unchanged) until the next
+ * blocking call on the plan (last_loss, logits, weights, grads, overflow,
+ * set_weights, get/set_optimizer_state) reports RT_ERR_LABEL once and clears
+ * the flag. */
 int rt_mlp_step(rt_mlp* mlp, const rt_buf* x, const rt_buf* labels);
 /* GpuMlp::forward_only (mod.rs:1514-1521). */
 int rt_mlp_forward(rt_mlp* mlp, const rt_buf* x);
 /* GpuMlp::logits (mod.rs:1524-1526): blocking, n = batch*classes floats. */
 int rt_mlp_logits(rt_mlp* mlp, float* host, size_t n);
 /* GpuMlp::last_loss (mod.rs:1529-1531): blocking; mean of the per-row
- * losses summed in row order.  Returns RT_ERR_LABEL if a label was >= C. */
+ * losses summed in row order.  Returns RT_ERR_LABEL if a label was >= C
+ * (see rt_mlp_step). */
 int rt_mlp_last_loss(rt_mlp* mlp, float* out);
 /* GpuMlp::weights / grads (mod.rs:1534-1551): blocking; host[i] receives
  * parameter i of [W1, b1, W2, b2, ...] (f32; the master copy for bf16;
  * gradients are reported unscaled when a loss scale is set). */
 int rt_mlp_weights(rt_mlp* mlp, float* const* host, int n);
 int rt_mlp_grads(rt_mlp* mlp, float* const* host, int n);
+/* The plan's stored intermediates of the last step (or forward), blocking,
+ * as n = batch x dims[layer+1] f32 values.  rt_mlp_activation: layer < n-1
+ * gives the hidden activation A = ReLU(Z) the plan keeps for the next layer
+ * and the ReLU mask (bf16 values widened exactly under RT_PREC_BF16), the
+ * last layer the logits (= GpuMlp::logits, mod.rs:1524-1526).  rt_mlp_delta:
+ * δ = ∂L/∂Z of that layer as the backward GEMMs read it (bf16 under
+ * RT_PREC_BF16, and then multiplied by the loss scale).  No counterpart in
+ * the reference beyond logits: they let a caller check each GEMM of the step
+ * on its own inputs. */
+int rt_mlp_activation(rt_mlp* mlp, int layer, float* host, size_t n);
+int rt_mlp_delta(rt_mlp* mlp, int layer, float* host, size_t n);
 /* GpuMlp::dispatches_por_passo (mod.rs:1559-1561): kernel launches per step. */
 int rt_mlp_dispatches(rt_mlp* mlp, int* out);
 /* Whether the last completed step was skipped for a non-finite gradient
@@ -307,8 +325,10 @@ int rt_empty(rt_ctx* ctx, rt_dtype dtype, const size_t* shape, int rank, rt_buf*
  * on a copy stream, into one of two device slots that alternate.  The call
  * first waits (on the host) for the last step that read the same slot, two
  * steps back, so the copy runs while the step on the other slot computes.
- * The host buffers may be reused on return.  rt_mlp_step_loaded runs rt_mlp_step on the most recently loaded
- * batch after its copy; it may be called again on the same batch. */
+ * The host buffers may be reused on return.  A label >= the number of
+ * classes is rejected here (RT_ERR_LABEL, nothing is loaded).
+ * rt_mlp_step_loaded runs rt_mlp_step on the most recently loaded batch after
+ * its copy; it may be called again on the same batch. */
 int rt_mlp_load(rt_mlp* mlp, const void* x, size_t x_bytes, const uint64_t* labels, size_t n);
 int rt_mlp_step_loaded(rt_mlp* mlp);
 

@@ -127,6 +127,9 @@ def lib() -> C.CDLL:
         "ocpu_mlp_forward": (C.c_int, [C.c_void_p, F32P, C.c_size_t, F32P]),
         "ocpu_mlp_get": (C.c_int, [C.c_void_p, C.c_int, C.c_int, F32P]),
         "ocpu_mlp_logits": (C.c_int, [C.c_void_p, F32P]),
+        "ocpu_mlp_set": (C.c_int, [C.c_void_p, C.c_int, C.c_int, F32P]),
+        "ocpu_mlp_get_t": (C.c_int, [C.c_void_p]),
+        "ocpu_mlp_set_t": (None, [C.c_void_p, C.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -480,12 +483,37 @@ class CpuMlp:
         return out
 
     def grads(self) -> List[np.ndarray]:
+        return self._get_all(1)
+
+    def _get_all(self, which: int) -> List[np.ndarray]:
         out = []
         for i in range(2 * self.n_layers):
             a = np.empty(self._shape(i), np.float32)
-            _check(lib().ocpu_mlp_get(self._h, 1, i, _p(a)))
+            _check(lib().ocpu_mlp_get(self._h, which, i, _p(a)))
             out.append(a)
         return out
+
+    def _set_all(self, which: int, arrays) -> None:
+        assert len(arrays) == 2 * self.n_layers
+        for i, a in enumerate(arrays):
+            a = f32(a).reshape(self._shape(i))
+            _check(lib().ocpu_mlp_set(self._h, which, i, _p(a)))
+
+    def set_weights(self, arrays) -> None:
+        """``Param::set`` (tape.rs:119-121) on every parameter, [W1, b1, ...]."""
+        self._set_all(0, arrays)
+
+    def optimizer_state(self):
+        """The optimizer's state after the steps so far: (m, v, t) for Adam
+        (optim.rs:143-149, 163), (velocity, [], 0) for Sgd.  Parameters not
+        updated yet read as zeros."""
+        return self._get_all(2), self._get_all(3), int(lib().ocpu_mlp_get_t(self._h))
+
+    def set_optimizer_state(self, m, v, t: int) -> None:
+        self._set_all(2, m)
+        if v is not None:
+            self._set_all(3, v)
+        lib().ocpu_mlp_set_t(self._h, int(t))
 
 
 # ------------------------------------------------------------------ data helpers

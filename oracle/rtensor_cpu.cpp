@@ -1059,24 +1059,60 @@ int ocpu_mlp_forward(void* p, const float* x, size_t batch, float* logits) {
   });
   return 0;
 }
-// which: 0 = parameter value, 1 = gradient of the last step; idx over [W¹, b¹, …].
+// The optimizer's per-parameter state map that `which` names: 2 = Adam m or
+// Sgd velocity, 3 = Adam v (optim.rs:100-103, 143-149: keyed by the param,
+// created as zeros on its first update).
+static std::unordered_map<size_t, Tensor>& opt_state_map(Mlp* m, int which) {
+  if (which == 2) return m->opt.kind == 1 ? m->opt.velocity : m->opt.m;
+  if (which == 3) return m->opt.v;
+  throw std::runtime_error("unknown state kind");
+}
+// which: 0 = parameter value, 1 = gradient of the last step, 2 = Adam m (Sgd
+// velocity), 3 = Adam v (zeros before the parameter's first update); idx over
+// [W¹, b¹, …].
 int ocpu_mlp_get(void* p, int which, int idx, float* out) {
   auto* m = static_cast<Mlp*>(p);
   OC_TRY({
     std::vector<size_t> ps = m->params();
     size_t pid = ps.at((size_t)idx);
+    const Tensor& th = *param_ref(pid).value;
     if (which == 0) {
-      const Tensor& t = *param_ref(pid).value;
-      std::memcpy(out, t.data.data(), t.len() * sizeof(float));
-    } else {
+      std::memcpy(out, th.data.data(), th.len() * sizeof(float));
+    } else if (which == 1) {
       if (!m->last) throw std::runtime_error("no step has run");
       const Tensor* g = m->last->grad_of_param(pid);
       if (!g) throw std::runtime_error("parameter has no gradient");
       std::memcpy(out, g->data.data(), g->len() * sizeof(float));
+    } else {
+      auto& st = opt_state_map(m, which);
+      auto it = st.find(pid);
+      if (it == st.end()) std::memset(out, 0, th.len() * sizeof(float));
+      else std::memcpy(out, it->second.data.data(), th.len() * sizeof(float));
     }
   });
   return 0;
 }
+// The inverse for which = 0 (Param::set, tape.rs:119-121), 2 and 3.
+int ocpu_mlp_set(void* p, int which, int idx, const float* in) {
+  auto* m = static_cast<Mlp*>(p);
+  OC_TRY({
+    std::vector<size_t> ps = m->params();
+    size_t pid = ps.at((size_t)idx);
+    Tensor& th = *param_ref(pid).value;
+    if (which == 0) {
+      std::memcpy(th.data.data(), in, th.len() * sizeof(float));
+    } else if (which == 2 || which == 3) {
+      Tensor t(th.shape, std::vector<float>(in, in + th.len()));
+      opt_state_map(m, which)[pid] = std::move(t);
+    } else {
+      throw std::runtime_error("gradients cannot be set");
+    }
+  });
+  return 0;
+}
+// Adam's step count t (optim.rs:163).
+int ocpu_mlp_get_t(void* p) { return static_cast<Mlp*>(p)->opt.t; }
+void ocpu_mlp_set_t(void* p, int t) { static_cast<Mlp*>(p)->opt.t = t; }
 int ocpu_mlp_logits(void* p, float* out) {
   auto* m = static_cast<Mlp*>(p);
   OC_TRY({

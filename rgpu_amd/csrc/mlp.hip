@@ -105,8 +105,11 @@ struct rt_mlp {
   } slot[2];
   bool slots_ready = false;
   int next_slot = 0, loaded = -1;
-  // Mixed precision: [0] applied Adam updates, [1] overflow flag of the last
-  // step, [2] a step was issued (see step_begin_launch).
+  // Device state words: [0] applied Adam updates, [1] overflow flag of the
+  // last step, [2] a step was issued (mixed precision, see step_begin_launch);
+  // [3] label flag: a loss of this plan saw a label >= the classes (sticky
+  // until reported; every update is skipped while it is set); [4] updates
+  // skipped while it was set (f32 plans, whose t lives on the host).
   int* state = nullptr;
   int t = 0;
   int dispatches = 0;
@@ -207,7 +210,7 @@ static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float s
       Launch Lz(c, "head_xent");
       hipError_t e = head_xent_launch(c->stream, (const float*)in, (int)Ly.din, p->theta + Ly.w_off, bias,
                                       labels ? (const uint32_t*)labels->ptr : nullptr, (float*)Ly.act, Ly.delta,
-                                      p->loss_rows, B, (int)Ly.dout, scale / (float)B, c->d_flags);
+                                      p->loss_rows, B, (int)Ly.dout, scale / (float)B, p->state + 3);
       if (e != hipSuccess) return hip_fail(c, e, "head_xent");
       return RT_OK;
     }
@@ -222,7 +225,7 @@ static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float s
     Layer& top = p->L[nl - 1];
     Launch Lz(c, "softmax_xent");
     hipError_t e = xent_launch(c->stream, (const float*)top.act, (const uint32_t*)labels->ptr, top.delta, top.delta_h,
-                               p->loss_rows, B, (int)top.dout, scale / (float)B, c->d_flags, (int)top.ldh);
+                               p->loss_rows, B, (int)top.dout, scale / (float)B, p->state + 3, (int)top.ldh);
     if (e != hipSuccess) return hip_fail(c, e, "softmax_xent");
   }
   return RT_OK;
@@ -672,10 +675,15 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
     P.skip_flag = overflow;
     P.device_t = p->state;
   }
+  // A label >= the classes skips the update (weights and moments stay as
+  // they were); an f32 plan counts the skipped step so that the report can
+  // take it back out of t.
+  P.skip_flag2 = p->state + 3;
   if (P.kind == 1 && P.momentum == 0.0f)
     for (auto& T : ts) T.m = nullptr;
   for (size_t i0 = 0; i0 < ts.size(); i0 += kMaxOptTensors) {
     const int nt = (int)std::min<size_t>(kMaxOptTensors, ts.size() - i0);
+    P.skip_count = (!p->mixed && i0 == 0) ? p->state + 4 : nullptr;
     Launch Lz(c, "optimizer");
     hipError_t e = optimizer_launch(c->stream, ts.data() + i0, nt, P);
     if (e != hipSuccess) return hip_fail(c, e, "optimizer");
@@ -694,8 +702,10 @@ int rt_mlp_load(rt_mlp* p, const void* x, size_t x_bytes, const uint64_t* labels
   auto& s = p->slot[k];
   if (x_bytes != s.x.bytes) return fail(c, RT_ERR_SHAPE, "batch of %zu bytes, plan takes %zu", x_bytes, s.x.bytes);
   if (n != p->batch) return fail(c, RT_ERR_SHAPE, "%zu labels, plan takes %zu", n, p->batch);
+  const size_t classes = p->L[p->n_layers - 1].dout;
   for (size_t i = 0; i < n; ++i)
-    if (labels[i] > 0xffffffffULL) return fail(c, RT_ERR_LABEL, "label %zu does not fit u32", i);
+    if (labels[i] >= classes) return fail(c, RT_ERR_LABEL, "label %zu is %llu, >= the %zu classes", i,
+                                          (unsigned long long)labels[i], classes);
   // The staging buffers are free once this slot's previous copy has run.
   if (s.copy_pending) HIP_TRY(c, hipEventSynchronize(s.copied), "staging wait");
   std::memcpy(s.x_host, x, x_bytes);
@@ -728,6 +738,25 @@ int rt_mlp_step_loaded(rt_mlp* p) {
   return RT_OK;
 }
 
+// The label flag of the plan, read on the host (blocking).  If a loss saw a
+// label >= the classes, the updates skipped since are taken back out of an
+// f32 plan's t (a mixed plan's device count never included them), the flag
+// is cleared, and RT_ERR_LABEL is returned: every blocking call on the plan
+// reports it once.
+static int report_label(rt_mlp* p) {
+  rt_ctx* c = p->ctx;
+  int st[5] = {0, 0, 0, 0, 0};
+  HIP_TRY(c, hipMemcpyAsync(st, p->state, sizeof st, hipMemcpyDeviceToHost, c->stream), "label flag");
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "label flag");
+  if (st[3] == 0) return RT_OK;
+  if (!p->mixed) p->t -= st[4];
+  // Mixed: the pending step (state[2]) was skipped, so it must not be counted.
+  HIP_TRY(c, fill_i32_launch(c->stream, p->state + 2, 0, 3), "label flag reset");
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "label flag reset");
+  return fail(c, RT_ERR_LABEL, "a label was >= the number of classes (%zu); the update was skipped",
+              p->L[p->n_layers - 1].dout);
+}
+
 int rt_mlp_forward(rt_mlp* p, const rt_buf* x) {
   if (p == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
@@ -742,29 +771,72 @@ int rt_mlp_logits(rt_mlp* p, float* host, size_t n) {
   rt_ctx* c = p->ctx;
   const Layer& top = p->L[p->n_layers - 1];
   if (host == nullptr || n != p->batch * top.dout) return fail(c, RT_ERR_SHAPE, "logits need %zu floats", p->batch * top.dout);
+  int rc = report_label(p);
+  if (rc) return rc;
   hipError_t e = hipMemcpyAsync(host, top.act, n * 4, hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "logits");
   return RT_OK;
 }
 
+// Copies one stored [batch, width] intermediate to host f32: bf16 values are
+// widened exactly; a padded row stride (the bf16 output layer's δ) is dropped.
+static int copy_rows_f32(rt_mlp* p, const void* src, bool half, size_t ld, size_t width, float* host) {
+  rt_ctx* c = p->ctx;
+  const size_t rows = p->batch;
+  if (!half) {
+    HIP_TRY(c, hipMemcpy2DAsync(host, width * 4, src, ld * 4, width * 4, rows, hipMemcpyDeviceToHost, c->stream),
+            "intermediate");
+    HIP_TRY(c, hipStreamSynchronize(c->stream), "intermediate");
+    return RT_OK;
+  }
+  std::vector<uint16_t> tmp(rows * width);
+  HIP_TRY(c, hipMemcpy2DAsync(tmp.data(), width * 2, src, ld * 2, width * 2, rows, hipMemcpyDeviceToHost, c->stream),
+          "intermediate");
+  HIP_TRY(c, hipStreamSynchronize(c->stream), "intermediate");
+  for (size_t i = 0; i < tmp.size(); ++i) {
+    const uint32_t u = (uint32_t)tmp[i] << 16;
+    std::memcpy(host + i, &u, 4);
+  }
+  return RT_OK;
+}
+
+int rt_mlp_activation(rt_mlp* p, int layer, float* host, size_t n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
+  rt_ctx* c = p->ctx;
+  if (layer < 0 || layer >= p->n_layers) return fail(c, RT_ERR_INVALID, "layer %d out of range", layer);
+  const Layer& Ly = p->L[layer];
+  if (host == nullptr || n != p->batch * Ly.dout) return fail(c, RT_ERR_SHAPE, "need %zu floats", p->batch * Ly.dout);
+  int rc = report_label(p);
+  if (rc) return rc;
+  const bool half = p->mixed && layer < p->n_layers - 1;
+  return copy_rows_f32(p, Ly.act, half, Ly.dout, Ly.dout, host);
+}
+
+int rt_mlp_delta(rt_mlp* p, int layer, float* host, size_t n) {
+  if (p == nullptr) return RT_ERR_INVALID;
+  bind_device(p->ctx);
+  rt_ctx* c = p->ctx;
+  if (layer < 0 || layer >= p->n_layers) return fail(c, RT_ERR_INVALID, "layer %d out of range", layer);
+  const Layer& Ly = p->L[layer];
+  if (host == nullptr || n != p->batch * Ly.dout) return fail(c, RT_ERR_SHAPE, "need %zu floats", p->batch * Ly.dout);
+  int rc = report_label(p);
+  if (rc) return rc;
+  if (p->mixed) return copy_rows_f32(p, Ly.delta_h, true, Ly.ldh, Ly.dout, host);
+  return copy_rows_f32(p, Ly.delta, false, Ly.dout, Ly.dout, host);
+}
+
 int rt_mlp_last_loss(rt_mlp* p, float* out) {
   if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
   rt_ctx* c = p->ctx;
+  int rc = report_label(p);
+  if (rc) return rc;
   std::vector<float> rows(p->batch);
-  int flag = 0;
   hipError_t e = hipMemcpyAsync(rows.data(), p->loss_rows, p->batch * 4, hipMemcpyDeviceToHost, c->stream);
-  if (e == hipSuccess) e = hipMemcpyAsync(&flag, c->d_flags, sizeof(int), hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
   if (e != hipSuccess) return hip_fail(c, e, "last_loss");
-  if (flag != 0) {
-    // Sticky until reported: clear it so later steps start clean.
-    e = fill_i32_launch(c->stream, c->d_flags, 0, 1);
-    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-    if (e != hipSuccess) return hip_fail(c, e, "flag reset");
-    return fail(c, RT_ERR_LABEL, "a label was >= the number of classes (%zu)", p->L[p->n_layers - 1].dout);
-  }
   // Tensor::mean_all (tensor.rs:284-286): sequential f32 sum, then divide.
   float s = 0.0f;
   for (float r : rows) s += r;
@@ -807,7 +879,9 @@ static int put(rt_mlp* p, float* base, const float* const* host, int n) {
 int rt_mlp_set_weights(rt_mlp* p, const float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
-  int rc = put(p, p->theta, host, n);
+  int rc = report_label(p);
+  if (rc) return rc;
+  rc = put(p, p->theta, host, n);
   if (rc || !p->mixed) return rc;
   rt_ctx* c = p->ctx;
   hipError_t e = convert_launch(c->stream, p->theta, RT_F32, p->theta_h, RT_BF16, p->n_params);
@@ -820,7 +894,8 @@ int rt_mlp_get_optimizer_state(rt_mlp* p, float* const* m, float* const* v, int 
   if (p == nullptr || t == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
   rt_ctx* c = p->ctx;
-  int rc;
+  int rc = report_label(p);
+  if (rc) return rc;
   if (m != nullptr && (rc = fetch(p, p->m, m, n))) return rc;
   if (v != nullptr && (rc = fetch(p, p->v, v, n))) return rc;
   if (!p->mixed) {
@@ -842,7 +917,8 @@ int rt_mlp_set_optimizer_state(rt_mlp* p, const float* const* m, const float* co
   bind_device(p->ctx);
   rt_ctx* c = p->ctx;
   if (t < 0) return fail(c, RT_ERR_INVALID, "t must be >= 0");
-  int rc;
+  int rc = report_label(p);
+  if (rc) return rc;
   if (m != nullptr && (rc = put(p, p->m, m, n))) return rc;
   if (v != nullptr && (rc = put(p, p->v, v, n))) return rc;
   p->t = t;
@@ -858,13 +934,17 @@ int rt_mlp_set_optimizer_state(rt_mlp* p, const float* const* m, const float* co
 int rt_mlp_weights(rt_mlp* p, float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
+  int rc = report_label(p);
+  if (rc) return rc;
   return fetch(p, p->theta, host, n);
 }
 
 int rt_mlp_grads(rt_mlp* p, float* const* host, int n) {
   if (p == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
-  int rc = fetch(p, p->grad, host, n);
+  int rc = report_label(p);
+  if (rc) return rc;
+  rc = fetch(p, p->grad, host, n);
   if (rc || !p->mixed || p->cfg.loss_scale == 1.0f) return rc;
   // Gradients are held scaled by the loss scale; report dL/dθ.
   const float inv = 1.0f / p->cfg.loss_scale;
@@ -887,6 +967,8 @@ int rt_mlp_overflow(rt_mlp* p, int* out) {
   if (p == nullptr || out == nullptr) return RT_ERR_INVALID;
   bind_device(p->ctx);
   rt_ctx* c = p->ctx;
+  int rc = report_label(p);
+  if (rc) return rc;
   int flag = 0;
   hipError_t e = hipMemcpyAsync(&flag, p->state + 1, sizeof(int), hipMemcpyDeviceToHost, c->stream);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);

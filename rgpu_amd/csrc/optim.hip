@@ -14,7 +14,8 @@
 //   m = m·β1 + g·(1−β1);  v = v·β2 + (g·g)·(1−β2);
 //   θ = θ − ((m·(1/c1)) / (√(v·(1/c2)) + ε))·lr
 // Under loss scaling the gradient is first multiplied by 1/scale (a power of
-// two, exact) and the whole update is skipped when the overflow flag is set.
+// two, exact) and the whole update is skipped when the overflow flag is set;
+// a training plan also skips it when its loss saw a label >= the classes.
 
 #include <algorithm>
 
@@ -81,7 +82,10 @@ __device__ inline void update(const rt::OptParams& P, Coef c, float graw, float&
 // Each thread owns 4 consecutive elements: one float4 of every stream when
 // the tensor allows it (T.vec), else four scalars.
 __global__ __launch_bounds__(kThreads) void optimizer_kernel(OptBatch b) {
-  if (b.p.skip_flag != nullptr && *b.p.skip_flag != 0) return;
+  if ((b.p.skip_flag != nullptr && *b.p.skip_flag != 0) || (b.p.skip_flag2 != nullptr && *b.p.skip_flag2 != 0)) {
+    if (b.p.skip_count != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *b.p.skip_count += 1;
+    return;
+  }
   Coef c{b.p.inv_c1, b.p.inv_c2};
   if (b.p.device_t != nullptr) {
     const int t = *b.p.device_t + 1;
@@ -171,7 +175,7 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(NonFiniteArgs a) {
 
 __global__ void step_begin_kernel(int* state) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    if (state[2] != 0 && state[1] == 0) state[0] += 1;
+    if (state[2] != 0 && state[1] == 0 && state[3] == 0) state[0] += 1;
     state[2] = 1;
     state[1] = 0;
   }

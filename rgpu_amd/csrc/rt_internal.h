@@ -198,14 +198,19 @@ struct OptParams {
   float lr = 0, beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, momentum = 0;
   float inv_c1 = 1, inv_c2 = 1;  // Adam bias corrections, 1/(1-β^t) in f32
   float grad_scale = 1;          // multiplies g first (1/loss_scale), exact for powers of two
-  const int* skip_flag = nullptr;  // if non-null and *skip_flag != 0, the update is skipped
+  // If either flag is non-null and set, the update is skipped; the first
+  // launch of a step may then count the skipped step in *skip_count (one
+  // thread of block 0 adds 1).
+  const int* skip_flag = nullptr;
+  const int* skip_flag2 = nullptr;
+  int* skip_count = nullptr;
   // If non-null, Adam's bias corrections come from the device step count
   // (*device_t + 1 = this update's t) instead of inv_c1 / inv_c2.
   const int* device_t = nullptr;
 };
 // Mixed-precision step prologue on state[0] = applied updates t, state[1] =
-// overflow flag, state[2] = a step was issued: t += (issued && !overflow);
-// issued = 1; overflow = 0.  One thread.
+// overflow flag, state[2] = a step was issued, state[3] = label flag:
+// t += (issued && !overflow && !label); issued = 1; overflow = 0.  One thread.
 hipError_t step_begin_launch(hipStream_t s, int* state);
 constexpr int kMaxOptTensors = 24;
 hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const OptParams& p);

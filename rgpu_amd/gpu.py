@@ -86,6 +86,8 @@ SIGNATURES = {
     "rt_mlp_step": (C.c_int, [_VP, _VP, _VP]),
     "rt_mlp_forward": (C.c_int, [_VP, _VP]),
     "rt_mlp_logits": (C.c_int, [_VP, C.POINTER(C.c_float), C.c_size_t]),
+    "rt_mlp_activation": (C.c_int, [_VP, C.c_int, C.POINTER(C.c_float), C.c_size_t]),
+    "rt_mlp_delta": (C.c_int, [_VP, C.c_int, C.POINTER(C.c_float), C.c_size_t]),
     "rt_mlp_last_loss": (C.c_int, [_VP, C.POINTER(C.c_float)]),
     "rt_mlp_weights": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.c_int]),
     "rt_mlp_grads": (C.c_int, [_VP, C.POINTER(C.POINTER(C.c_float)), C.c_int]),
@@ -523,6 +525,13 @@ class GpuMlp:
             lib().rt_mlp_destroy(self._h)
         self._h = None
 
+    def _live(self):
+        """The plan's handle; raises once the plan or its Gpu is gone (a
+        closed context releases its models, so the handle would dangle)."""
+        if not self._h or not self.gpu._h:
+            raise RtError(2, "the model was destroyed or its Gpu was closed")
+        return self._h
+
     def __del__(self):
         try:
             self.destroy()
@@ -530,7 +539,7 @@ class GpuMlp:
             pass
 
     def step(self, x: GpuTensor, labels: GpuTensor) -> None:
-        self.gpu._call("rt_mlp_step", self._h, x.handle, labels.handle)
+        self.gpu._call("rt_mlp_step", self._live(), x.handle, labels.handle)
 
     def carregar(self, x, labels) -> None:
         """GpuMlp::carregar (mod.rs:1486-1495), overlapped: stage a host batch
@@ -543,26 +552,41 @@ class GpuMlp:
             host = x.astype(np.float32, copy=False)
         host = np.ascontiguousarray(host)
         lab = np.ascontiguousarray(np.asarray(labels).astype(np.uint64))
-        self.gpu._call("rt_mlp_load", self._h, host.ctypes.data_as(C.c_void_p), host.nbytes,
+        self.gpu._call("rt_mlp_load", self._live(), host.ctypes.data_as(C.c_void_p), host.nbytes,
                        lab.ctypes.data_as(C.POINTER(C.c_uint64)), lab.size)
 
-    load = carregar
+    load = carregar  # the batch loader, rt_mlp_load (checkpoints: save_checkpoint / load_checkpoint)
 
     def step_loaded(self) -> None:
         """rt_mlp_step on the most recently loaded batch."""
-        self.gpu._call("rt_mlp_step_loaded", self._h)
+        self.gpu._call("rt_mlp_step_loaded", self._live())
 
     def forward_only(self, x: GpuTensor) -> None:
-        self.gpu._call("rt_mlp_forward", self._h, x.handle)
+        self.gpu._call("rt_mlp_forward", self._live(), x.handle)
+
+    def activation(self, layer: int) -> np.ndarray:
+        """The stored activation of ``layer`` (ReLU output of a hidden layer,
+        logits of the last), f32 [batch, width]."""
+        out = np.empty((self.lote, self.dims[layer + 1]), np.float32)
+        self.gpu._call("rt_mlp_activation", self._live(), int(layer), out.ctypes.data_as(C.POINTER(C.c_float)),
+                       out.size)
+        return out
+
+    def delta(self, layer: int) -> np.ndarray:
+        """δ = ∂L/∂Z of ``layer`` as the backward GEMMs read it (under bf16,
+        the bf16 values times the loss scale), f32 [batch, width]."""
+        out = np.empty((self.lote, self.dims[layer + 1]), np.float32)
+        self.gpu._call("rt_mlp_delta", self._live(), int(layer), out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
+        return out
 
     def logits(self) -> np.ndarray:
         out = np.empty((self.lote, self.dims[-1]), np.float32)
-        self.gpu._call("rt_mlp_logits", self._h, out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
+        self.gpu._call("rt_mlp_logits", self._live(), out.ctypes.data_as(C.POINTER(C.c_float)), out.size)
         return out
 
     def last_loss(self) -> float:
         v = C.c_float()
-        self.gpu._call("rt_mlp_last_loss", self._h, C.byref(v))
+        self.gpu._call("rt_mlp_last_loss", self._live(), C.byref(v))
         return v.value
 
     def _shapes(self):
@@ -574,7 +598,7 @@ class GpuMlp:
     def _fetch(self, fn: str) -> List[np.ndarray]:
         arrs = [np.empty(s, np.float32) for s in self._shapes()]
         ptrs = (C.POINTER(C.c_float) * len(arrs))(*[a.ctypes.data_as(C.POINTER(C.c_float)) for a in arrs])
-        self.gpu._call(fn, self._h, ptrs, len(arrs))
+        self.gpu._call(fn, self._live(), ptrs, len(arrs))
         return arrs
 
     def weights(self) -> List[np.ndarray]:
@@ -599,19 +623,19 @@ class GpuMlp:
     def set_weights(self, arrs) -> None:
         """Param::set (tape.rs:119-121) for every parameter, in parameter order."""
         arrs = self._checked(arrs)
-        self.gpu._call("rt_mlp_set_weights", self._h, self._ptrs(arrs), len(arrs))
+        self.gpu._call("rt_mlp_set_weights", self._live(), self._ptrs(arrs), len(arrs))
 
     def optimizer_state(self):
         """(m, v, t): the optimizer's moments per parameter and the applied-update count."""
         m = [np.empty(s, np.float32) for s in self._shapes()]
         v = [np.empty(s, np.float32) for s in self._shapes()]
         t = C.c_int()
-        self.gpu._call("rt_mlp_get_optimizer_state", self._h, self._ptrs(m), self._ptrs(v), len(m), C.byref(t))
+        self.gpu._call("rt_mlp_get_optimizer_state", self._live(), self._ptrs(m), self._ptrs(v), len(m), C.byref(t))
         return m, v, t.value
 
     def set_optimizer_state(self, m, v, t: int) -> None:
         m, v = self._checked(m), self._checked(v)
-        self.gpu._call("rt_mlp_set_optimizer_state", self._h, self._ptrs(m), self._ptrs(v), len(m), int(t))
+        self.gpu._call("rt_mlp_set_optimizer_state", self._live(), self._ptrs(m), self._ptrs(v), len(m), int(t))
 
     def state_dict(self) -> dict:
         """Everything a resumed run needs: weights, optimizer moments and t."""
@@ -622,7 +646,7 @@ class GpuMlp:
         self.set_weights(state["weights"])
         self.set_optimizer_state(state["m"], state["v"], state["t"])
 
-    def save(self, path: str) -> None:
+    def save_checkpoint(self, path: str) -> None:
         """Checkpoint to an .npz file (plain arrays, no pickled objects)."""
         st = self.state_dict()
         arrays = {"t": np.array([st["t"]], np.int64)}
@@ -631,7 +655,7 @@ class GpuMlp:
                 arrays[f"{key}_{i}"] = a
         np.savez(path, **arrays)
 
-    def load(self, path: str) -> None:
+    def load_checkpoint(self, path: str) -> None:
         n = len(self._shapes())
         with np.load(path, allow_pickle=False) as z:
             st = {key: [z[f"{key}_{i}"] for i in range(n)] for key in ("weights", "m", "v")}
@@ -643,10 +667,10 @@ class GpuMlp:
 
     def dispatches_por_passo(self) -> int:
         v = C.c_int()
-        self.gpu._call("rt_mlp_dispatches", self._h, C.byref(v))
+        self.gpu._call("rt_mlp_dispatches", self._live(), C.byref(v))
         return v.value
 
     def overflow(self) -> bool:
         v = C.c_int()
-        self.gpu._call("rt_mlp_overflow", self._h, C.byref(v))
+        self.gpu._call("rt_mlp_overflow", self._live(), C.byref(v))
         return bool(v.value)

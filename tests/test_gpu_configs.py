@@ -16,7 +16,8 @@ import pytest
 
 from oracle import oracle as O
 from rgpu_amd import gpu as G
-from tests.gpu_common import bf16_pipeline_grads, kaiming_model, normal_batch, oracle_threads, uniform_labels
+from tests.gpu_common import (bf16_pipeline_grads, bf16_plan_layer_checks, grad_gate, kaiming_model, normal_batch,
+                              oracle_threads, uniform_labels)
 
 pytestmark = pytest.mark.gpu
 
@@ -67,7 +68,42 @@ def test_splitk_dw_f16(gpu, K, slices):
     assert np.array_equal(gpu.download(dw2), got_w)
 
 
-def _mixed_step_check(gpu, dims, B, steps, lr, seed, emu_bound=1e-2):
+def bf16_gates(mlp, cpu, params_r, x, lab, col_frac=None, emu_bound=None):
+    """Step-1 gradient gates of the bf16 plan.
+
+    1. Layer-local: every GEMM and rounding point of the step on the plan's
+       own stored inputs, per element against float64 (pins the kernels).
+    2. Against the f32 oracle (the 2e-2 bar), scale-aware: per tensor
+       norm-wise and max-relative distance.  bf16 activation storage alone
+       flips ReLU masks (~0.1% of them at these sizes), which moves the first
+       layers' gradients up to ~12% norm-wise from f32; the float64
+       restatement of the bf16 pipeline measures that inherent distance for
+       each tensor, and the plan may deviate from f32 by at most
+       max(2e-2, 2 x) it.  A zeroed or wrong tensor scores ~1.
+    3. Optionally (small widths, where f32-vs-float64 accumulation does not
+       flip masks) norm-wise against that restatement itself."""
+    gg, gc = mlp.grads(), cpu.grads()
+    bf16_plan_layer_checks(mlp, params_r, x, lab, 1024.0)
+    emu = bf16_pipeline_grads(params_r, x, lab, col_frac=col_frac)
+    inh_n, inh_m = [], []
+    for i, (e, c) in enumerate(zip(emu, gc)):
+        if isinstance(e, tuple):
+            e, cols = e
+            c = c[:, cols]
+        c = c.astype(np.float64)
+        inh_n.append(float(np.linalg.norm(e - c) / np.linalg.norm(c)))
+        inh_m.append(float(np.abs(e - c).max() / np.abs(c).max()))
+    print("inherent bf16 distance from f32 (float64 restatement): norm-wise", ["%.1e" % v for v in inh_n],
+          "\n  max-relative", ["%.1e" % v for v in inh_m], flush=True)
+    grad_gate("bf16 step-1 grads vs the f32 oracle", gc, gg, [max(2e-2, 2 * v) for v in inh_n],
+              [max(2e-2, 2 * v) for v in inh_m], erro_bound=2e-2)
+    if emu_bound is not None:
+        ne = [float(np.linalg.norm(a - b) / max(np.linalg.norm(a), 1e-30)) for a, b in zip(emu, gg)]
+        print("  norm-wise vs the bf16 restatement", ["%.1e" % r for r in ne], flush=True)
+        assert max(ne) < emu_bound
+
+
+def _mixed_step_check(gpu, dims, B, steps, lr, seed, emu_bound=1e-2, col_frac=None):
     params = kaiming_model(seed, dims)
     # the CPU reference runs in f32 from the bf16-rounded initial weights and inputs
     params_r = [bf16_round(p) if i % 2 == 0 else p for i, p in enumerate(params)]
@@ -82,22 +118,7 @@ def _mixed_step_check(gpu, dims, B, steps, lr, seed, emu_bound=1e-2):
         lc = cpu.step(x, lab)
         lg = mlp.last_loss()
         if s == 0:
-            gg, gc = mlp.grads(), cpu.grads()
-            # the reference's parity metric (gpu.rs:53-60) against the f32 CPU path
-            er = [O.erro_rel(a, b) for a, b in zip(gc, gg)]
-            # norm-wise distance to f32 (what bf16 storage costs), and to the
-            # float64 restatement of the bf16 pipeline (pins the implementation)
-            emu = bf16_pipeline_grads(params_r, x, lab)
-            nf = [float(np.linalg.norm(a - b) / max(np.linalg.norm(a), 1e-30)) for a, b in zip(gc, gg)]
-            ne = [float(np.linalg.norm(a - b) / max(np.linalg.norm(a), 1e-30)) for a, b in zip(emu, gg)]
-            print("step 1 grads: erro_rel vs f32", ["%.1e" % r for r in er], "\n  norm vs f32",
-                  ["%.1e" % r for r in nf], "\n  norm vs bf16 pipeline", ["%.1e" % r for r in ne], flush=True)
-            assert max(er) < 2e-2
-            # At large widths the first layers' gradients are so sensitive that
-            # f32-vs-float64 accumulation flipping a bf16 rounding is visible;
-            # the restatement check is only discriminating at small width.
-            if emu_bound is not None:
-                assert max(ne) < emu_bound
+            bf16_gates(mlp, cpu, params_r, x, lab, col_frac=col_frac, emu_bound=emu_bound)
             assert not mlp.overflow()
         losses.append((lc, lg))
     return losses, cpu, mlp
@@ -123,15 +144,52 @@ def test_mixed_precision_mlp_trajectory_small(gpu):
     assert max(ew) < 0.1
 
 
-def test_mixed_precision_mlp_full_size_steps(gpu):
-    # 8 x 4096 ReLU layers -> 1000 classes, batch 4096: two steps at full size
-    # (the f32 oracle takes ~10 s per step on 16 threads).
+def test_mixed_precision_mlp_full_size_step(gpu):
+    # 8 x 4096 ReLU layers -> 1000 classes, batch 4096: the first step at full
+    # size against the f32 oracle (~10 s on 16 threads), with the layer-local
+    # checks and the float64 bf16 restatement on 1/8 of each dW's columns.
     dims = [4096] * 9 + [1000]
     t0 = time.time()
-    losses, cpu, mlp = _mixed_step_check(gpu, dims, 4096, 2, 1e-3, 6, emu_bound=None)
+    losses, cpu, mlp = _mixed_step_check(gpu, dims, 4096, 1, 1e-3, 6, emu_bound=None, col_frac=0.125)
     d = [abs(a - b) / abs(a) for a, b in losses]
-    print("full size losses", losses, "rel diff", ["%.1e" % x for x in d], f"{time.time() - t0:.0f}s")
+    print("full size loss", losses, "rel diff", ["%.1e" % x for x in d], f"{time.time() - t0:.0f}s")
     assert max(d) < 2e-2
+
+
+def test_mixed_precision_mlp_full_size_100_step_trajectory(gpu):
+    """tests/golden/c5_trajectory.json holds the oracle's f32 losses of 100
+    Adam steps of the 8 x 4096 -> 1000 MLP at batch 4096 from bf16-rounded
+    weights and inputs (written by make_c5_trajectory.py beside it).  The bf16
+    plan (f32 master weights, loss scale 1024) runs the same 100 steps; every
+    loss must stay within 2e-2 relative of the oracle's (the tests/gpu.rs:
+    99-139 pattern at the bf16 bar)."""
+    import concurrent.futures as cf
+    import json
+    import os
+    from tests.golden import make_c5_trajectory as mk
+
+    with open(os.path.join(os.path.dirname(mk.__file__), "c5_trajectory.json")) as f:
+        fix = json.load(f)
+    want = [float(np.uint32(b).view(np.float32)) for b in fix["loss_bits"]]
+    assert len(want) == mk.STEPS
+    mlp = G.GpuMlp.from_params(gpu, mk.initial_params(), mk.BATCH, mk.LR, precision="bf16", loss_scale=1024.0)
+    t0 = time.time()
+    got = []
+    with cf.ThreadPoolExecutor(8) as ex:  # the Rng fills run in C, outside the GIL
+        futs = [ex.submit(mk.batch, s) for s in range(mk.STEPS)]
+        for s, fu in enumerate(futs):
+            x, lab = fu.result()
+            mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, lab))
+            got.append(mlp.last_loss())
+            futs[s] = None
+            if s % 10 == 0:
+                print(f"step {s}: oracle {want[s]:.5f} bf16 {got[-1]:.5f} ({time.time() - t0:.0f} s)", flush=True)
+    d = [abs(g - w) / abs(w) for g, w in zip(got, want)]
+    i = int(np.argmax(d))
+    print(f"100-step trajectory: max rel diff {d[i]:.2e} at step {i} (oracle {want[i]:.5f}, bf16 {got[i]:.5f}); "
+          f"final {want[-1]:.5f} vs {got[-1]:.5f}", flush=True)
+    assert max(d) <= 2e-2
+    assert not mlp.overflow()
 
 
 @pytest.mark.parametrize("dims,batch", [
@@ -192,7 +250,9 @@ def test_linear4096_backward_bf16_full_size(gpu):
     # Against the f32 inputs before rounding: within 2e-2.
     f_dx = (dy32[i].astype(np.float64) * w32[j].astype(np.float64)).sum(1)
     f_dw = (x32[:, p].astype(np.float64) * dy32[:, q].astype(np.float64)).sum(0)
-    e_dx = np.max(np.abs(g_dx - f_dx)) / np.max(np.abs(f_dx))
-    e_dw = np.max(np.abs(g_dw - f_dw)) / np.max(np.abs(f_dw))
-    print(f"vs f32 inputs: dX {e_dx:.2e}, dW {e_dw:.2e}", flush=True)
-    assert e_dx <= 2e-2 and e_dw <= 2e-2
+    # Scale-aware (a zeroed or wrong result scores ~1): max-relative and
+    # norm-wise over the samples, and for db over the whole vector.
+    f_db = dy32.sum(0, keepdims=True, dtype=np.float64)
+    rows = grad_gate("c3 vs the f32 inputs (dX, dW samples; db)", [f_dx, f_dw, f_db],
+                     [g_dx, g_dw, got_db.astype(np.float64)], 2e-2, 2e-2)
+    print(f"vs f32 inputs: dX {rows[0][1]:.2e}, dW {rows[1][1]:.2e} max-relative", flush=True)

@@ -508,3 +508,43 @@ def test_oracle_reproduces_committed_mlp_vectors():
     assert got.keys() == want.keys()
     for name in want:
         assert got[name] == want[name], name
+
+
+def test_adam_state_export_closed_form_and_resume():
+    # optim.rs:162-198: after one step m = g·(1−β1), v = (g·g)·(1−β2) exactly
+    # (m₀ = v₀ = 0), t = 1; the state exported after k steps and loaded into
+    # a fresh model continues bit for bit like the uninterrupted run.
+    rng = O.Rng(3)
+    layers = [O.Dense(8, 16, "relu", rng), O.Dense(16, 4, "linear", rng)]
+    params = [p.value() for l in layers for p in l.params()]
+    x = np.sin(np.arange(64 * 8, dtype=np.float32) * np.float32(0.37)).reshape(64, 8)
+    lab = (np.arange(64) % 4).astype(np.uint32)
+    a = O.CpuMlp(params[0::2], params[1::2])
+    a.set_optimizer("adam", 1e-2)
+    a.step(x, lab)
+    m, v, t = a.optimizer_state()
+    assert t == 1
+    for g, mi, vi in zip(a.grads(), m, v):
+        assert np.array_equal(mi, g * np.float32(1.0 - np.float32(0.9)))
+        assert np.array_equal(vi, (g * g) * np.float32(1.0 - np.float32(0.999)))
+    for s in range(4):
+        a.step(x, (lab + s) % 4)
+    m, v, t = a.optimizer_state()
+    assert t == 5
+    b = O.CpuMlp(params[0::2], params[1::2])
+    b.set_optimizer("adam", 1e-2)
+    b.set_weights(a.weights())
+    b.set_optimizer_state(m, v, t)
+    for s in range(3):
+        la, lb = a.step(x, (lab + 2 * s) % 4), b.step(x, (lab + 2 * s) % 4)
+        assert la == lb
+    for wa, wb in zip(a.weights(), b.weights()):
+        assert np.array_equal(wa, wb)
+    # the resumed run differs if t is not restored (bias corrections)
+    c = O.CpuMlp(params[0::2], params[1::2])
+    c.set_optimizer("adam", 1e-2)
+    c.set_weights(b.weights())
+    c.set_optimizer_state(*b.optimizer_state()[:2], 0)
+    c.step(x, lab)
+    b.step(x, lab)
+    assert any(not np.array_equal(wb, wc) for wb, wc in zip(b.weights(), c.weights()))
