@@ -125,6 +125,17 @@ int rt_linear_backward(rt_ctx* ctx, const rt_buf* x, const rt_buf* delta, const 
  * elements.  colsum as in rt_gemm (RT_TN only). */
 int rt_gemm_splitk(rt_ctx* ctx, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* c,
                    rt_buf* partials, size_t slices, rt_buf* colsum);
+/* rt_gemm_splitk for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving or training loops, harnesses that forbid
+ * hipMalloc); no counterpart in the reference.  The same kernels and results,
+ * bit for bit, but the partial planes (and the half GEMM's column-sum shares)
+ * live in a static 64 MiB device array of the library: each GPU it runs on
+ * holds its own copy until the process ends.  The call allocates nothing; it
+ * returns RT_ERR_SHAPE when slices·M·N + slices·N (+ the shares) floats
+ * exceed 64 MiB.  Calls that overlap on one GPU (other contexts, other
+ * threads) share the array and race; calls on one context are ordered. */
+int rt_gemm_splitk_static(rt_ctx* ctx, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* c,
+                          size_t slices, rt_buf* colsum);
 /* fatias_sugeridas (mod.rs:1079-1088), re-derived for 256 CUs. */
 size_t rt_splitk_slices(size_t m, size_t n, size_t k);
 

@@ -30,6 +30,7 @@ SOURCES = {
     "rowops.hip": ["-ffp-contract=off"],
     "optim.hip": ["-ffp-contract=off"],
     "tensor_ops.hip": ["-ffp-contract=off"],
+    "noalloc.hip": [],
 }
 
 COMMON = [

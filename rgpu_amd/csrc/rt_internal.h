@@ -56,6 +56,8 @@ struct rt_ctx {
   // Host-to-device copies of staged batches (rt_mlp_load), created on first
   // use; default priority like the main stream.
   hipStream_t copy_stream = nullptr;
+  // This device's copy of rt_gemm_splitk_static's static scratch array.
+  float* static_scratch = nullptr;
 };
 
 namespace rt {
@@ -67,6 +69,19 @@ int hip_fail(rt_ctx* c, hipError_t e, const char* what);
 // Makes c->scratch hold at least elems floats (grow-only; waits for queued
 // work before replacing a smaller one).
 int ensure_scratch(rt_ctx* c, size_t elems);
+
+// The split-K GEMM behind rt_gemm_splitk and rt_gemm_splitk_static: argument
+// checks, then the launches with the partial planes at part (slices·M·N, then
+// slices·N column-sum rows) and, for a half TN product with column sums, the
+// column-sum shares at cs_scratch (cs_elems floats; 0 for none).
+int splitk_check(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, const rt_buf* out, size_t slices,
+                 const rt_buf* colsum, size_t* M, size_t* N, size_t* K);
+int splitk_run(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, size_t slices,
+               rt_buf* colsum, size_t M, size_t N, size_t K, float* part, float* cs_scratch, size_t cs_elems);
+// noalloc.hip: the device address of the static scratch array on the current
+// device, and its size in floats.
+hipError_t static_scratch_address(float** out);
+size_t static_scratch_floats();
 
 // HIP's current device is per thread: every entry point makes the context's
 // device current first, so a context works from any thread and next to a

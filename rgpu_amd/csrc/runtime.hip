@@ -130,6 +130,9 @@ int rt_open(int device, rt_ctx** out) {
   c->name = props.name;
   c->num_cus = props.multiProcessorCount;
   e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  // The device address of this device's copy of the static scratch array
+  // of rt_gemm_splitk_static (loads its code object on this device).
+  if (e == hipSuccess) e = static_scratch_address(&c->static_scratch);
   if (e == hipSuccess) e = hipMalloc(&c->d_flags, 64 * sizeof(int));
   if (e == hipSuccess) e = fill_i32_launch(c->stream, c->d_flags, 0, 64);
   if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
@@ -542,24 +545,27 @@ size_t rt_splitk_slices(size_t m, size_t n, size_t k) {
   return std::max<size_t>(s, 1);
 }
 
-int rt_gemm_splitk(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, rt_buf* partials,
-                   size_t slices, rt_buf* colsum) {
-  CHECK_CTX(c);
-  if (!a || !b || !out || !partials) return fail(c, RT_ERR_INVALID, "null buffer");
+}  // extern "C"
+
+namespace rt {
+
+int splitk_check(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, const rt_buf* out, size_t slices,
+                 const rt_buf* colsum, size_t* M, size_t* N, size_t* K) {
   if (layout != RT_NN && layout != RT_TN) return fail(c, RT_ERR_INVALID, "split-K takes RT_NN or RT_TN");
   if (slices < 1 || slices > 1024) return fail(c, RT_ERR_INVALID, "slices must be in [1, 1024]");
-  size_t M, N, K;
-  int rc = gemm_shapes(c, layout, a, b, &M, &N, &K);
+  int rc = gemm_shapes(c, layout, a, b, M, N, K);
   if (rc) return rc;
-  if (out->n != M * N || out->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "C must be f32 [%zu,%zu]", M, N);
+  if (out->n != *M * *N || out->dtype != RT_F32) return fail(c, RT_ERR_SHAPE, "C must be f32 [%zu,%zu]", *M, *N);
   if (a->dtype != b->dtype || a->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "A and B must share a float dtype");
-  if (partials->dtype != RT_F32 || partials->n < slices * M * N + (colsum ? slices * N : 0))
-    return fail(c, RT_ERR_SHAPE, "partials need %zu f32 elements", slices * M * N + (colsum ? slices * N : 0));
   if (colsum) {
     if (layout != RT_TN) return fail(c, RT_ERR_INVALID, "fused colsum is only for the TN layout");
-    if (colsum->dtype != RT_F32 || colsum->n != N) return fail(c, RT_ERR_SHAPE, "colsum must be f32 [%zu]", N);
+    if (colsum->dtype != RT_F32 || colsum->n != *N) return fail(c, RT_ERR_SHAPE, "colsum must be f32 [%zu]", *N);
   }
-  if (M == 0 || N == 0) return RT_OK;
+  return RT_OK;
+}
+
+int splitk_run(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, size_t slices,
+               rt_buf* colsum, size_t M, size_t N, size_t K, float* part, float* cs_scratch, size_t cs_elems) {
   GemmDesc d;
   d.layout = layout;
   d.in_dtype = a->dtype;
@@ -572,11 +578,9 @@ int rt_gemm_splitk(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b
   d.lda = (int)a->shape[1];
   d.ldb = (int)b->shape[1];
   d.ldc = (int)N;
-  float* part = static_cast<float*>(partials->ptr);
-  if (colsum && is_half(a->dtype)) {
-    if ((rc = ensure_scratch(c, colsum_scratch_need(d.M, d.N, (int)slices)))) return rc;
-    d.cs_scratch = c->scratch;
-    d.cs_scratch_elems = c->scratch_elems;
+  if (colsum && is_half(a->dtype) && cs_elems > 0) {
+    d.cs_scratch = cs_scratch;
+    d.cs_scratch_elems = cs_elems;
   }
   if (slices == 1) {
     d.C = out->ptr;
@@ -600,6 +604,27 @@ int rt_gemm_splitk(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b
                                colsum ? static_cast<float*>(colsum->ptr) : nullptr),
           "split-K reduce");
   return RT_OK;
+}
+
+}  // namespace rt
+
+extern "C" {
+
+int rt_gemm_splitk(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, rt_buf* partials,
+                   size_t slices, rt_buf* colsum) {
+  CHECK_CTX(c);
+  if (!a || !b || !out || !partials) return fail(c, RT_ERR_INVALID, "null buffer");
+  size_t M, N, K;
+  int rc = splitk_check(c, layout, a, b, out, slices, colsum, &M, &N, &K);
+  if (rc) return rc;
+  if (partials->dtype != RT_F32 || partials->n < slices * M * N + (colsum ? slices * N : 0))
+    return fail(c, RT_ERR_SHAPE, "partials need %zu f32 elements", slices * M * N + (colsum ? slices * N : 0));
+  if (M == 0 || N == 0) return RT_OK;
+  if (colsum && is_half(a->dtype)) {
+    if ((rc = ensure_scratch(c, colsum_scratch_need((int)M, (int)N, (int)slices)))) return rc;
+  }
+  return splitk_run(c, layout, a, b, out, slices, colsum, M, N, K, static_cast<float*>(partials->ptr), c->scratch,
+                    (colsum && is_half(a->dtype)) ? c->scratch_elems : 0);
 }
 
 // ------------------------------------------------------------------ row / column ops

@@ -72,6 +72,7 @@ SIGNATURES = {
     "rt_convert": (C.c_int, [_VP, _VP, _VP]),
     "rt_gemm": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, C.c_int, _VP, _VP]),
     "rt_gemm_splitk": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, _VP, C.c_size_t, _VP]),
+    "rt_gemm_splitk_static": (C.c_int, [_VP, C.c_int, _VP, _VP, _VP, C.c_size_t, _VP]),
     "rt_splitk_slices": (C.c_size_t, [C.c_size_t, C.c_size_t, C.c_size_t]),
     "rt_colsum": (C.c_int, [_VP, _VP, _VP]),
     "rt_bias_add": (C.c_int, [_VP, _VP, _VP]),
@@ -357,6 +358,12 @@ class Gpu:
         """ops_split_k (mod.rs:1095-1146)."""
         self._call("rt_gemm_splitk", self._h, TN if transposta else NN, a.handle, b.handle, c.handle,
                    partials.handle, slices, colsum.handle if colsum else None)
+
+    def split_k_static(self, a, b, c, slices: int, transposta: bool, colsum: Optional[GpuTensor] = None):
+        """split_k with its partial planes in the library's static device
+        array: allocates nothing (rt_gemm_splitk_static)."""
+        self._call("rt_gemm_splitk_static", self._h, TN if transposta else NN, a.handle, b.handle, c.handle, slices,
+                   colsum.handle if colsum else None)
 
     def linear_backward(self, x, delta, w, dx, dw, db=None):
         """dW = Xᵀδ, db = 1ᵀδ, dX = δWᵀ of a Linear layer (one launch when the
