@@ -1,6 +1,7 @@
 """Benchmark of the MLP training step on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only all|step|bwd|splitk|mixed|tape|pcie]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                    [--only all|step|small|bwd|splitk|mixed|tape|pcie|copy]
 
 Workload (one "step"): MLP 512->1024(ReLU)->1024(ReLU)->10, f32, batch 2048,
 softmax cross-entropy, Adam(1e-3, 0.9, 0.999, 1e-8): forward, backward and the
@@ -8,9 +9,16 @@ optimizer update, on synthetic N(0,1) batches with uniform labels in [0,10)
 that are resident in HBM before timing starts (one fresh batch per step).
 
 Prints ONE JSON line.  `value` is ms/step over K timed steps (lower is
-better).  Next to it:
+better), timed after the W warmup steps and a further ~100 ms of steps that
+let the device settle at its sustained clock (settle_steps in the line).
+Next to it:
   roofline      the dominant kernel of the step: algorithmic FLOPs per launch
-                over its average HIP-event duration, against the f32 MFMA peak
+                over its average duration, from HIP events that the kernel's
+                own dispatch carries (hipExtLaunchKernel), against the f32
+                MFMA peak
+  small_batch   the same MLP at batch 32 with SGD(0.01), one step = forward,
+                backward, update: ms/step, per-launch µs, the HBM roofline of
+                its compulsory bytes, and its own CPU baseline
   bwd_gemm      Linear 4096->4096 backward at batch 8192 in bf16 (dX = dY·Wᵀ,
                 dW = Xᵀ·dY with db fused), TFLOP/s against the bf16 MFMA peak
   splitk_dw     dW = Xᵀ·dY, K = 262144, f16 in / f32 out, db fused, against
@@ -23,7 +31,9 @@ better).  Next to it:
                 256, Adam) trained through the device autodiff tape, one
                 HIP launch per recorded op, against the oracle's CPU tape
   cpu_baseline  the CPU oracle (C++ restatement of rtensor's single-threaded
-                CPU path) timed on a bounded sample of the same workload
+                CPU path) timed on a bounded sample of the same workload, on
+                one host thread; bwd_gemm, splitk_dw and mixed_mlp carry
+                their own, from row samples scaled to the whole workload
 """
 from __future__ import annotations
 
@@ -100,6 +110,7 @@ def bench_step(gpu, G, steps, warmup):
     for i in range(warmup):
         mlp.step(xs[i % nb], ys[i % nb])
     gpu.sync()
+    settle = settle_clock(gpu, lambda i: mlp.step(xs[i % nb], ys[i % nb]))
     t0 = time.perf_counter()
     for i in range(steps):
         mlp.step(xs[(warmup + i) % nb], ys[(warmup + i) % nb])
@@ -117,7 +128,83 @@ def bench_step(gpu, G, steps, warmup):
     gpu.profile(False)
     prof = gpu.perfilar()
     gpu.profile_reset()
-    return wall, loss, prof, mlp.dispatches_por_passo()
+    return wall, loss, prof, mlp.dispatches_por_passo(), settle
+
+
+def settle_clock(gpu, work, ms=100.0):
+    """Runs work(i) in batches until ~ms of device load have passed: the
+    device takes ~25 ms of sustained load to settle at its clock (~1.95 GHz
+    at the ~1.35 kW socket limit), and the first launches run up to 15%
+    slower.  Returns {settle_ms, settle_steps}."""
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            work(n)
+            n += 1
+        gpu.sync()
+    return {"settle_ms": round((time.perf_counter() - t0) * 1e3, 1), "settle_steps": n}
+
+
+def c1_bytes(dims):
+    """Compulsory HBM bytes of one SGD step: W read by the forward and again
+    by dX (layers > 0), dW written, and the update reading θ and g and
+    writing θ (12 B per parameter)."""
+    w = sum(dims[l] * dims[l + 1] for l in range(len(dims) - 1))
+    b = sum(dims[1:])
+    w_dx = sum(dims[l] * dims[l + 1] for l in range(1, len(dims) - 1))
+    return 4 * (w + b) + 4 * w_dx + 4 * (w + b) + 12 * (w + b)
+
+
+def bench_small(gpu, G, steps=2000, warmup=100):
+    """MLP 512-1024-1024-10, f32, batch 32, SGD(0.01): the one-step config of
+    README.md:50, timed over many steps (one fresh resident batch each)."""
+    B = 32
+    rng = np.random.default_rng(32)
+    params = []
+    for l in range(len(DIMS) - 1):
+        params += [kaiming(rng, DIMS[l], DIMS[l + 1]), np.zeros((1, DIMS[l + 1]), np.float32)]
+    mlp = G.GpuMlp.from_params(gpu, params, B, 0.01, optimizer="sgd")
+    nb = 64
+    xs = [gpu.upload(rng.standard_normal((B, DIMS[0]), dtype=np.float32)) for _ in range(nb)]
+    ys = [G.upload_labels(gpu, rng.integers(0, DIMS[-1], B)) for _ in range(nb)]
+    for i in range(warmup):
+        mlp.step(xs[i % nb], ys[i % nb])
+    gpu.sync()
+    settle = settle_clock(gpu, lambda i: mlp.step(xs[i % nb], ys[i % nb]))
+    t0 = time.perf_counter()
+    for i in range(steps):
+        mlp.step(xs[i % nb], ys[i % nb])
+    gpu.sync()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    gpu.timer_begin()
+    for i in range(steps):
+        mlp.step(xs[i % nb], ys[i % nb])
+    dev_ms = gpu.timer_end() / steps
+    gpu.profile_reset()
+    gpu.profile(True)
+    for i in range(200):
+        mlp.step(xs[i % nb], ys[i % nb])
+    gpu.sync()
+    gpu.profile(False)
+    prof = gpu.perfilar()
+    gpu.profile_reset()
+    launches = mlp.dispatches_por_passo()
+    mlp.destroy()
+    byts = c1_bytes(DIMS)
+    gbs = byts / (ms * 1e-3) / 1e9
+    kern = {n: round(t / c * 1e3, 2) for n, c, t in prof}
+    return {"config": "MLP 512-1024(ReLU)-1024(ReLU)-10, f32, batch 32, SGD(0.01); one step = forward, "
+                      "backward, update", "ms_per_step": round(ms, 4), "device_ms_per_step": round(dev_ms, 4),
+            "launches_per_step": launches, "kernels_us": kern,
+            "kernel_sum_us": round(sum(kern.values()), 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "bytes_per_step": byts,
+                         "note": "a chain of dependent launches: the step is bound by launch latency, "
+                                 "not by these bytes"},
+            "vs_published": {"ref_gpu_ms": 0.73, "ref_cpu_ms": 14.01,
+                             "source": "README.md:50, rtensor wgpu on an RTX 4070 Laptop and its CPU path"},
+            **settle}
 
 
 def bench_bwd_gemm(gpu, G, reps=10, rounds=20):
@@ -212,6 +299,7 @@ def bench_mixed(gpu, G, steps=20, warmup=10):
     for i in range(warmup):
         mlp.step(xs[i % 4], ys[i % 4])
     gpu.sync()
+    settle = settle_clock(gpu, lambda i: mlp.step(xs[i % 4], ys[i % 4]))
     t0 = time.perf_counter()
     for i in range(steps):
         mlp.step(xs[i % 4], ys[i % 4])
@@ -223,7 +311,8 @@ def bench_mixed(gpu, G, steps=20, warmup=10):
     return {"config": "MLP 8x4096(ReLU) -> 1000, batch 4096, bf16 weights/activations, f32 master, "
                       "loss scale 1024, Adam(1e-3)", "ms_per_step": round(ms, 3),
             "tflops": round(flops / (ms * 1e-3) / 1e12, 1), "peak_tflops": PEAK_BF16_TFLOPS,
-            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "final_loss": round(float(loss), 4)}
+            "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "final_loss": round(float(loss), 4),
+            **settle}
 
 
 # examples/bench_grande.rs: N samples of D features, two ReLU layers of H,
@@ -383,6 +472,120 @@ def bench_copy(gpu, G, mib=256, reps=5):
     return {"bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4, "launches": reps}
 
 
+def host_cpu():
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return cpu
+
+
+def cpu_small_baseline(budget_s=3.0):
+    """The oracle's batch-32 SGD step (tests/gpu.rs:116-121 order), 1 thread."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    rng = np.random.default_rng(32)
+    params = []
+    for l in range(len(DIMS) - 1):
+        params += [kaiming(rng, DIMS[l], DIMS[l + 1]), np.zeros((1, DIMS[l + 1]), np.float32)]
+    m = O.CpuMlp(params[0::2], params[1::2])
+    m.set_optimizer("sgd", 0.01)
+    x = rng.standard_normal((32, DIMS[0]), dtype=np.float32)
+    y = rng.integers(0, DIMS[-1], 32).astype(np.uint32)
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < budget_s and n < 400:
+        m.step(x, y)
+        n += 1
+    ms = (time.perf_counter() - t0) / n * 1e3
+    return {"value": round(ms, 3), "unit": "ms/step", "cores": 1, "kind": "port",
+            "sample": f"{n} batch-32 SGD steps on the oracle, 1 thread on {host_cpu()}"}
+
+
+def cpu_bwd_baseline(rows=512):
+    """The CPU path of a Linear 4096->4096 backward (ops.rs:125-129: g·Wᵀ and
+    Xᵀ·g, then reduce_to for db) on `rows` of the 8192 batch rows, 1 thread,
+    scaled by 8192 / rows (every term is linear in the batch).  f32 on the
+    same values (the CPU path has no bf16)."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    B, D = 8192, 4096
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((rows, D), dtype=np.float32) / np.float32(64.0)
+    g = rng.standard_normal((rows, D), dtype=np.float32) / np.float32(64.0)
+    w = rng.uniform(-np.sqrt(6.0 / D), np.sqrt(6.0 / D), size=(D, D)).astype(np.float32)
+    wt = np.ascontiguousarray(w.T)
+    t0 = time.perf_counter()
+    O.matmul(g, wt)
+    O.matmul(np.ascontiguousarray(x.T), g)
+    O.reduce_to(g, (1, D))
+    s = time.perf_counter() - t0
+    ms = s * B / rows * 1e3
+    return {"value": round(ms, 1), "unit": "ms per backward (dX + dW + db)", "cores": 1, "kind": "port",
+            "sample": f"{rows} of the 8192 rows on the oracle (g·Wᵀ, Xᵀ·g, reduce_to), 1 thread, "
+                      f"{s:.2f} s scaled x{B // rows}"}
+
+
+def cpu_splitk_baseline(rows=16384):
+    """dW = Xᵀ·dY and db = reduce_to(dY) on the oracle over `rows` of the
+    262144 reduction rows, 1 thread, scaled by 262144 / rows."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    K, M, N = 262144, 512, 512
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((rows, M), dtype=np.float32) / np.float32(16.0)
+    dy = rng.standard_normal((rows, N), dtype=np.float32) / np.float32(16.0)
+    t0 = time.perf_counter()
+    O.matmul(np.ascontiguousarray(x.T), dy)
+    O.reduce_to(dy, (1, N))
+    s = time.perf_counter() - t0
+    return {"value": round(s * K / rows * 1e3, 1), "unit": "ms per dW + db", "cores": 1, "kind": "port",
+            "sample": f"{rows} of the 262144 rows on the oracle, 1 thread, {s:.2f} s scaled x{K // rows}"}
+
+
+def cpu_mixed_baseline(batches=(16, 48)):
+    """One training step of the 8 x 4096 -> 1000 MLP on the oracle (f32, the
+    CPU path has no bf16), 1 thread, at two small batches; the step time is
+    a + b·batch (the Adam sweep over 138.3 M parameters and the per-step
+    copies of the weights do not scale with the batch, the GEMMs do),
+    extrapolated to batch 4096, after one untimed step."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    dims = [4096] * 9 + [1000]
+    rng = np.random.default_rng(5)
+    params = []
+    for l in range(len(dims) - 1):
+        params += [kaiming(rng, dims[l], dims[l + 1]), np.zeros((1, dims[l + 1]), np.float32)]
+    m = O.CpuMlp(params[0::2], params[1::2])
+    del params
+    m.set_optimizer("adam", 1e-3)
+    # the first step also allocates Adam's m and v (1.1 GB): not timed
+    m.step(rng.standard_normal((batches[0], dims[0]), dtype=np.float32),
+           rng.integers(0, dims[-1], batches[0]).astype(np.uint32))
+    ts = []
+    for b in batches:
+        x = rng.standard_normal((b, dims[0]), dtype=np.float32)
+        y = rng.integers(0, dims[-1], b).astype(np.uint32)
+        t0 = time.perf_counter()
+        m.step(x, y)
+        ts.append(time.perf_counter() - t0)
+    del m
+    slope = (ts[1] - ts[0]) / (batches[1] - batches[0])
+    fixed = ts[0] - slope * batches[0]
+    full = fixed + slope * 4096
+    return {"value": round(full * 1e3, 0), "unit": "ms/step", "cores": 1, "kind": "port",
+            "sample": f"one oracle step at batch {batches[0]} ({ts[0]:.2f} s) and {batches[1]} ({ts[1]:.2f} s), "
+                      f"1 thread; a + b·batch extrapolated to 4096 (a = {fixed:.2f} s, b = {slope * 1e3:.1f} ms/row)"}
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's single-threaded training step on the host, bounded sample."""
     from oracle import oracle as O
@@ -404,15 +607,7 @@ def cpu_baseline(budget_s=12.0):
         if time.perf_counter() - t0 > budget_s or n >= 20:
             break
     ms = (time.perf_counter() - t0) / n * 1e3
-    cpu = platform.processor() or platform.machine()
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    cpu = host_cpu()
     return {"value": round(ms, 2), "unit": "ms/step", "cores": 1, "kind": "port",
             "sample": f"{n} steps of the batch-2048 Adam step, oracle C++ port of rtensor's CPU path, "
                       f"1 thread on {cpu} ({os.cpu_count()} logical CPUs visible)"}
@@ -424,7 +619,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "step", "bwd", "splitk", "mixed", "copy", "tape", "pcie"], default="all",
+    ap.add_argument("--only", choices=["all", "step", "small", "bwd", "splitk", "mixed", "copy", "tape", "pcie"],
+                    default="all",
                     help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
     ap.add_argument("--rounds", type=int, default=20,
                     help="rounds of the bf16 backward pair for --only bwd (more rounds hold the load for "
@@ -438,13 +634,13 @@ def main():
     from rgpu_amd import gpu as G
 
     gpu = G.Gpu(0)
-    if args.only in ("bwd", "splitk", "mixed", "copy", "tape", "pcie"):
-        fn = {"bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed, "copy": bench_copy,
-              "tape": bench_tape, "pcie": bench_pcie}[args.only]
+    if args.only in ("small", "bwd", "splitk", "mixed", "copy", "tape", "pcie"):
+        fn = {"small": bench_small, "bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed,
+              "copy": bench_copy, "tape": bench_tape, "pcie": bench_pcie}[args.only]
         res = fn(gpu, G, rounds=args.rounds) if args.only == "bwd" else fn(gpu, G)
         print(json.dumps({args.only: res}), flush=True)
         return
-    wall, loss, prof, launches = bench_step(gpu, G, args.steps, args.warmup)
+    wall, loss, prof, launches, settle = bench_step(gpu, G, args.steps, args.warmup)
     ms = wall / args.steps * 1e3
     total_flops = step_flops(DIMS, BATCH)
 
@@ -462,6 +658,8 @@ def main():
         achieved = flops / (avg_ms * 1e-3) / 1e12
         roof = {"kernel": name, "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_F32_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_F32_TFLOPS, 4), "traffic": traffic_for(name),
+                "traffic_source": "profiles/pmc_traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of "
+                                  "bench.py --only step, scaled by a copy kernel of known size",
                 "flops_per_launch": flops, "avg_us": round(avg_ms * 1e3, 2)}
     else:
         roof = {"kernel": name, "bound": "hbm", "achieved": None, "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -489,8 +687,11 @@ def main():
         "final_loss": round(float(loss), 5),
         "roofline": roof,
         "kernels_us": kernels,
+        "kernel_sum_us": round(sum(kernels.values()), 2),
+        **settle,
     }
     if args.only == "all":
+        out["small_batch"] = bench_small(gpu, G)
         out["bwd_gemm"] = bench_bwd_gemm(gpu, G)
         out["splitk_dw"] = bench_splitk(gpu, G)
         out["mixed_mlp"] = bench_mixed(gpu, G)
@@ -504,6 +705,23 @@ def main():
             ct = cpu_tape_baseline()
             out["tape_mlp"]["cpu_baseline"] = ct
             out["tape_mlp"]["speedup_vs_cpu"] = round(ct["value"] / out["tape_mlp"]["ms_per_step"], 1)
+        if "small_batch" in out:
+            c = cpu_small_baseline()
+            out["small_batch"]["cpu_baseline"] = c
+            out["small_batch"]["speedup_vs_cpu"] = round(c["value"] / out["small_batch"]["ms_per_step"], 1)
+        if "bwd_gemm" in out:
+            c = cpu_bwd_baseline()
+            out["bwd_gemm"]["cpu_baseline"] = c
+            out["bwd_gemm"]["speedup_vs_cpu"] = round(c["value"] / (out["bwd_gemm"]["dX_ms"] +
+                                                                    out["bwd_gemm"]["dW_db_ms"]), 1)
+        if "splitk_dw" in out:
+            c = cpu_splitk_baseline()
+            out["splitk_dw"]["cpu_baseline"] = c
+            out["splitk_dw"]["speedup_vs_cpu"] = round(c["value"] / out["splitk_dw"]["ms"], 1)
+        if "mixed_mlp" in out:
+            c = cpu_mixed_baseline()
+            out["mixed_mlp"]["cpu_baseline"] = c
+            out["mixed_mlp"]["speedup_vs_cpu"] = round(c["value"] / out["mixed_mlp"]["ms_per_step"], 1)
     print(json.dumps(out), flush=True)
 
 

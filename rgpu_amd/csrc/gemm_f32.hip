@@ -690,7 +690,7 @@ hipError_t launch_f32(hipStream_t s, F32Args a) {
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
   dim3 grid(a.tiles_m * a.tiles_n, 1, a.splits);
-  hipLaunchKernelGGL((gemm_f32_kernel<T>), grid, dim3(T::THREADS), 0, s, a);
+  rt::launch((gemm_f32_kernel<T>), grid, dim3(T::THREADS), 0, s, a);
   return hipGetLastError();
 }
 
@@ -726,7 +726,7 @@ hipError_t launch_dma(hipStream_t s, F32Args a) {
   a.tiles_m = a.M / 64;
   a.tiles_n = a.N / 64;
   dim3 grid(a.tiles_m * a.tiles_n, 1, a.splits);
-  hipLaunchKernelGGL((gemm_f32_kernel<T>), grid, dim3(T::THREADS), 0, s, a);
+  rt::launch((gemm_f32_kernel<T>), grid, dim3(T::THREADS), 0, s, a);
   return hipGetLastError();
 }
 
@@ -782,7 +782,7 @@ hipError_t launch_pair_tn_nt(hipStream_t s, F32Args a0, F32Args a1) {
   const long long nb1 = (long long)a1.tiles_m * a1.tiles_n * a1.splits;
   const long long n0 = (nb0 + 7) / 8 * 8;
   if (n0 + nb1 > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemm_f32_pair_kernel<T0, T1>), dim3((unsigned)(n0 + nb1)), dim3(T0::THREADS), 0, s, a0,
+  rt::launch((gemm_f32_pair_kernel<T0, T1>), dim3((unsigned)(n0 + nb1)), dim3(T0::THREADS), 0, s, a0,
                      a1, (int)n0);
   return hipGetLastError();
 }
@@ -826,7 +826,7 @@ hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits
   const long long total = (long long)M * N;
   int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partials, splits, stride, M, N,
+  rt::launch(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partials, splits, stride, M, N,
                      static_cast<float*>(C), ldc, epi, bias, static_cast<const float*>(mask), colsum_partials,
                      colsum);
   return hipGetLastError();

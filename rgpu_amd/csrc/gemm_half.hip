@@ -798,14 +798,14 @@ hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16, float* c
     a.cs_parts = cs_scratch;
   const dim3 grid(a.tiles_m * a.tiles_n, 1, splits), block(64 * WGM * WGN);
   if (bf16)
-    hipLaunchKernelGGL((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true, kDmaBK, kDmaStages>), grid, block, 0,
+    rt::launch((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true, kDmaBK, kDmaStages>), grid, block, 0,
                        s, a);
   else
-    hipLaunchKernelGGL((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false, kDmaBK, kDmaStages>), grid, block,
+    rt::launch((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false, kDmaBK, kDmaStages>), grid, block,
                        0, s, a);
   if (a.cs_parts) {
     const long long n = (long long)splits * a.N;
-    hipLaunchKernelGGL(cs_shares_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.cs_parts,
+    rt::launch(cs_shares_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.cs_parts,
                        a.tiles_m, splits, a.N, a.colsum, a.nf_flag);
   }
   return hipGetLastError();
@@ -816,9 +816,9 @@ hipError_t launch_regs(hipStream_t s, HalfArgs a, int splits, bool bf16) {
   set_tiles<BM, BN>(a);
   const dim3 grid(a.tiles_m * a.tiles_n, 1, splits), block(64 * WGM * WGN);
   if (bf16)
-    hipLaunchKernelGGL((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true>), grid, block, 0, s, a);
+    rt::launch((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, true>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false>), grid, block, 0, s, a);
+    rt::launch((gemm_half_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 

@@ -186,7 +186,7 @@ __global__ void step_begin_kernel(int* state) {
 namespace rt {
 
 hipError_t step_begin_launch(hipStream_t s, int* state) {
-  hipLaunchKernelGGL(step_begin_kernel, dim3(1), dim3(64), 0, s, state);
+  rt::launch(step_begin_kernel, dim3(1), dim3(64), 0, s, state);
   return hipGetLastError();
 }
 
@@ -226,7 +226,7 @@ hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const Op
   b.block_start[nt] = (int)blocks;
   if (blocks == 0) return hipSuccess;
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(optimizer_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, b);
+  rt::launch(optimizer_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, b);
   return hipGetLastError();
 }
 
@@ -243,7 +243,7 @@ hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const
   a.nt = nt;
   a.flag = flag;
   int blocks = (int)std::max<long long>(1, std::min<long long>((total + 255) / 256, 2048));
-  hipLaunchKernelGGL(nonfinite_kernel, dim3(blocks), dim3(256), 0, s, a);
+  rt::launch(nonfinite_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

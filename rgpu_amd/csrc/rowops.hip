@@ -302,17 +302,17 @@ hipError_t head_xent_launch(hipStream_t s, const float* A, int K, const float* W
   // 16 waves when K splits into 16 whole 16-k chunks per wave (shorter
   // dependent load chains per wave; the block count is fixed by the rows).
   if (K % 256 == 0)
-    hipLaunchKernelGGL(head_xent_kernel<16>, dim3(blocks), dim3(1024), 0, s, A, K, W, bias, labels, logits, delta,
+    rt::launch(head_xent_kernel<16>, dim3(blocks), dim3(1024), 0, s, A, K, W, bias, labels, logits, delta,
                        loss_rows, rows, cols, scale, err_flag);
   else
-    hipLaunchKernelGGL(head_xent_kernel<8>, dim3(blocks), dim3(512), 0, s, A, K, W, bias, labels, logits, delta,
+    rt::launch(head_xent_kernel<8>, dim3(blocks), dim3(512), 0, s, A, K, W, bias, labels, logits, delta,
                        loss_rows, rows, cols, scale, err_flag);
   return hipGetLastError();
 }
 
 hipError_t argmax_launch(hipStream_t s, const float* z, uint32_t* out, int rows, int cols) {
   if (rows < 1 || cols < 1) return hipSuccess;
-  hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, out, rows, cols);
+  rt::launch(argmax_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, z, out, rows, cols);
   return hipGetLastError();
 }
 
@@ -320,7 +320,7 @@ hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* label
                        float* loss_rows, int rows, int cols, float scale, int* err_flag, int ld_half) {
   if (rows <= 0) return hipSuccess;
   if (ld_half < cols) ld_half = cols;
-  hipLaunchKernelGGL(xent_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, logits, labels, delta,
+  rt::launch(xent_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, logits, labels, delta,
                      static_cast<unsigned short*>(delta_half), ld_half, loss_rows, rows, cols, scale, err_flag);
   return hipGetLastError();
 }
@@ -345,7 +345,7 @@ hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, in
                          size_t scratch_elems) {
   if (cols <= 0) return hipSuccess;
   if (rows <= 0) {
-    hipLaunchKernelGGL(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, (const float*)nullptr, 0, cols, dst);
+    rt::launch(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, (const float*)nullptr, 0, cols, dst);
     return hipGetLastError();
   }
   const int chunk = colsum_chunk(rows, cols);
@@ -354,50 +354,50 @@ hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, in
   if (parts > 1 && (scratch == nullptr || scratch_elems < (size_t)parts * cols)) return hipErrorInvalidValue;
   dim3 g1((cols + 255) / 256, parts);
   if (dtype == RT_F32)
-    hipLaunchKernelGGL(colsum_stage1<float>, g1, dim3(256), 0, s, static_cast<const float*>(src), rows, cols, chunk, out1);
+    rt::launch(colsum_stage1<float>, g1, dim3(256), 0, s, static_cast<const float*>(src), rows, cols, chunk, out1);
   else if (dtype == RT_BF16)
-    hipLaunchKernelGGL(colsum_stage1<unsigned short>, g1, dim3(256), 0, s, static_cast<const unsigned short*>(src),
+    rt::launch(colsum_stage1<unsigned short>, g1, dim3(256), 0, s, static_cast<const unsigned short*>(src),
                        rows, cols, chunk, out1);
   else
-    hipLaunchKernelGGL(colsum_stage1<_Float16>, g1, dim3(256), 0, s, static_cast<const _Float16*>(src), rows, cols,
+    rt::launch(colsum_stage1<_Float16>, g1, dim3(256), 0, s, static_cast<const _Float16*>(src), rows, cols,
                        chunk, out1);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || parts == 1) return e;
-  hipLaunchKernelGGL(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, scratch, parts, cols, dst);
+  rt::launch(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, scratch, parts, cols, dst);
   return hipGetLastError();
 }
 
 hipError_t bias_add_launch(hipStream_t s, float* z, const float* b, int rows, int cols) {
-  hipLaunchKernelGGL(bias_add_kernel, dim3(grid_for((long long)rows * cols)), dim3(256), 0, s, z, b, rows, cols);
+  rt::launch(bias_add_kernel, dim3(grid_for((long long)rows * cols)), dim3(256), 0, s, z, b, rows, cols);
   return hipGetLastError();
 }
 
 hipError_t relu_launch(hipStream_t s, const float* x, float* y, size_t n) {
-  hipLaunchKernelGGL(relu_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, x, y, (long long)n);
+  rt::launch(relu_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, x, y, (long long)n);
   return hipGetLastError();
 }
 
 hipError_t relu_bwd_launch(hipStream_t s, const void* a, int a_dtype, float* delta, size_t n) {
   if (a_dtype == RT_F32)
-    hipLaunchKernelGGL(relu_bwd_kernel<float>, dim3(grid_for((long long)n)), dim3(256), 0, s,
+    rt::launch(relu_bwd_kernel<float>, dim3(grid_for((long long)n)), dim3(256), 0, s,
                        static_cast<const float*>(a), delta, (long long)n);
   else if (a_dtype == RT_BF16)
-    hipLaunchKernelGGL(relu_bwd_kernel<unsigned short>, dim3(grid_for((long long)n)), dim3(256), 0, s,
+    rt::launch(relu_bwd_kernel<unsigned short>, dim3(grid_for((long long)n)), dim3(256), 0, s,
                        static_cast<const unsigned short*>(a), delta, (long long)n);
   else
-    hipLaunchKernelGGL(relu_bwd_kernel<_Float16>, dim3(grid_for((long long)n)), dim3(256), 0, s,
+    rt::launch(relu_bwd_kernel<_Float16>, dim3(grid_for((long long)n)), dim3(256), 0, s,
                        static_cast<const _Float16*>(a), delta, (long long)n);
   return hipGetLastError();
 }
 
 hipError_t convert_launch(hipStream_t s, const void* src, int src_dtype, void* dst, int dst_dtype, size_t n) {
-  hipLaunchKernelGGL(convert_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, src, src_dtype, dst, dst_dtype,
+  rt::launch(convert_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, src, src_dtype, dst, dst_dtype,
                      (long long)n);
   return hipGetLastError();
 }
 
 hipError_t fill_i32_launch(hipStream_t s, int* p, int v, size_t n) {
-  hipLaunchKernelGGL(fill_i32_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, p, v, (long long)n);
+  rt::launch(fill_i32_kernel, dim3(grid_for((long long)n)), dim3(256), 0, s, p, v, (long long)n);
   return hipGetLastError();
 }
 

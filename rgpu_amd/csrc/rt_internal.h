@@ -1,6 +1,7 @@
 // Internal declarations shared by the host runtime and the kernel sources.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdarg>
@@ -103,7 +104,31 @@ inline void bind_device(const rt_ctx* c) {
     if (_e != hipSuccess) return ::rt::hip_fail((c), _e, what); \
   } while (0)
 
-// Brackets one kernel launch with HIP events when profiling is on.
+// The events the kernel launches of the current profiled Launch scope carry
+// (per thread; null when not profiling): the first kernel takes `start`, every
+// kernel takes `stop`, so the pair spans the scope's kernels.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool used = false;
+};
+extern thread_local LaunchEvents* g_launch_events;
+
+// Every kernel of the library is launched through here.  While a profiled
+// Launch scope is open the kernel's own dispatch carries its events
+// (hipExtLaunchKernel timestamps the dispatch packet, the clock rocprofv3's
+// kernel trace reads), so profiling adds no marker packets between kernels.
+template <typename F, typename... Args>
+inline void launch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+  if (LaunchEvents* ev = g_launch_events) {
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, s, ev->used ? nullptr : ev->start, ev->stop, 0u, args...);
+    ev->used = true;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, s, args...);
+  }
+}
+
+// Labels the kernels launched in its scope for rt_profile_report when
+// profiling is on.
 class Launch {
  public:
   Launch(rt_ctx* c, const char* label);
@@ -114,7 +139,9 @@ class Launch {
  private:
   rt_ctx* c_;
   const char* label_;
-  hipEvent_t e0_ = nullptr;
+  LaunchEvents ev_;
+  LaunchEvents* prev_ = nullptr;
+  bool on_ = false;
 };
 
 // ---------------------------------------------------------------- GEMM

@@ -56,32 +56,41 @@ int ensure_scratch(rt_ctx* c, size_t elems) {
   return RT_OK;
 }
 
+thread_local LaunchEvents* g_launch_events = nullptr;
+
+static hipEvent_t take_event(rt_ctx* c) {
+  if (!c->event_pool.empty()) {
+    hipEvent_t e = c->event_pool.back();
+    c->event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
+
 Launch::Launch(rt_ctx* c, const char* label) : c_(c), label_(label) {
   if (!c_->profiling) return;
-  if (c_->event_pool.empty()) {
-    hipEvent_t e;
-    if (hipEventCreate(&e) != hipSuccess) return;
-    c_->event_pool.push_back(e);
+  ev_.start = take_event(c_);
+  ev_.stop = take_event(c_);
+  if (ev_.start == nullptr || ev_.stop == nullptr) {
+    if (ev_.start) c_->event_pool.push_back(ev_.start);
+    if (ev_.stop) c_->event_pool.push_back(ev_.stop);
+    return;
   }
-  e0_ = c_->event_pool.back();
-  c_->event_pool.pop_back();
-  hipEventRecord(e0_, c_->stream);
+  prev_ = g_launch_events;
+  g_launch_events = &ev_;
+  on_ = true;
 }
 
 Launch::~Launch() {
-  if (!c_->profiling || e0_ == nullptr) return;
-  hipEvent_t e1;
-  if (c_->event_pool.empty()) {
-    if (hipEventCreate(&e1) != hipSuccess) {
-      c_->event_pool.push_back(e0_);
-      return;
-    }
-  } else {
-    e1 = c_->event_pool.back();
-    c_->event_pool.pop_back();
+  if (!on_) return;
+  g_launch_events = prev_;
+  if (ev_.used) {
+    c_->prof.push_back(rt_prof_rec{std::string(label_), ev_.start, ev_.stop});
+  } else {  // nothing was launched in the scope
+    c_->event_pool.push_back(ev_.start);
+    c_->event_pool.push_back(ev_.stop);
   }
-  hipEventRecord(e1, c_->stream);
-  c_->prof.push_back(rt_prof_rec{std::string(label_), e0_, e1});
 }
 
 }  // namespace rt

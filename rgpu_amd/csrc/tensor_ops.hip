@@ -314,14 +314,14 @@ namespace rt {
 
 hipError_t unary_launch(hipStream_t s, int op, float k, const float* x, float* y, long long n) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(unary_kernel, dim3(grid_for(n)), dim3(256), 0, s, op, k, x, y, n);
+  rt::launch(unary_kernel, dim3(grid_for(n)), dim3(256), 0, s, op, k, x, y, n);
   return hipGetLastError();
 }
 
 hipError_t unary_vjp_launch(hipStream_t s, int op, float k, const float* g, const float* x, const float* y, float* dx,
                             long long n) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(unary_vjp_kernel, dim3(grid_for(n)), dim3(256), 0, s, op, k, g, x, y, dx, n);
+  rt::launch(unary_vjp_kernel, dim3(grid_for(n)), dim3(256), 0, s, op, k, g, x, y, dx, n);
   return hipGetLastError();
 }
 
@@ -330,9 +330,9 @@ hipError_t binary_launch_r(hipStream_t s, int op, const float* a, const float* b
                            long long n) {
   const dim3 grid(grid_for(n)), block(256);
   if (n < (1LL << 31))
-    hipLaunchKernelGGL((binary_kernel<R, int>), grid, block, 0, s, op, a, b, out, sh, (int)n);
+    rt::launch((binary_kernel<R, int>), grid, block, 0, s, op, a, b, out, sh, (int)n);
   else
-    hipLaunchKernelGGL((binary_kernel<R, long long>), grid, block, 0, s, op, a, b, out, sh, n);
+    rt::launch((binary_kernel<R, long long>), grid, block, 0, s, op, a, b, out, sh, n);
   return hipGetLastError();
 }
 
@@ -414,7 +414,7 @@ hipError_t reduce_to_launch(hipStream_t s, const float* g, const long long* gsha
     r.red_s[i] = src >= 0 ? red_s[src] : 0;
   }
   if (r.n_out <= 0) return hipSuccess;
-  hipLaunchKernelGGL(reduce_to_kernel, dim3(grid_for(r.n_out)), dim3(256), 0, s, g, out, r);
+  rt::launch(reduce_to_kernel, dim3(grid_for(r.n_out)), dim3(256), 0, s, g, out, r);
   return hipGetLastError();
 }
 
@@ -423,27 +423,27 @@ size_t sum_scratch_elems(long long n) { return (size_t)std::max<long long>(1, st
 hipError_t sum_all_launch(hipStream_t s, const float* x, long long n, float div, float* out, float* scratch) {
   const long long parts = (long long)sum_scratch_elems(n);
   const long long chunk = std::max<long long>(1, (n + parts - 1) / parts);
-  hipLaunchKernelGGL(sum_stage1, dim3((unsigned)parts), dim3(256), 0, s, x, n, chunk, scratch, div, out);
-  if (parts > 1) hipLaunchKernelGGL(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)parts, div, out);
+  rt::launch(sum_stage1, dim3((unsigned)parts), dim3(256), 0, s, x, n, chunk, scratch, div, out);
+  if (parts > 1) rt::launch(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)parts, div, out);
   return hipGetLastError();
 }
 
 hipError_t scalar_fill_launch(hipStream_t s, const float* scalar, float div, const float* x, float* out, long long n) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(scalar_fill_kernel, dim3(grid_for(n)), dim3(256), 0, s, scalar, div, x, out, n);
+  rt::launch(scalar_fill_kernel, dim3(grid_for(n)), dim3(256), 0, s, scalar, div, x, out, n);
   return hipGetLastError();
 }
 
 hipError_t softmax_rows_launch(hipStream_t s, const float* z, float* y, long long rows, long long cols) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, z, y, rows, cols);
+  rt::launch(softmax_rows_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, z, y, rows, cols);
   return hipGetLastError();
 }
 
 hipError_t softmax_rows_vjp_launch(hipStream_t s, const float* sm, const float* g, float* dx, long long rows,
                                    long long cols) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(softmax_rows_vjp_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, sm, g, dx, rows,
+  rt::launch(softmax_rows_vjp_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, sm, g, dx, rows,
                      cols);
   return hipGetLastError();
 }
@@ -453,16 +453,16 @@ hipError_t xent_logits_launch(hipStream_t s, const float* z, const float* y, flo
                               float dir_scale) {
   const long long blocks = std::max<long long>(1, (rows + 255) / 256);
   if (blocks > 1 && (size_t)blocks > scratch_elems) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(xent_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, z, y, dir, rows, cols, scratch, div,
+  rt::launch(xent_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, z, y, dir, rows, cols, scratch, div,
                      out, dir_scale);
-  if (blocks > 1) hipLaunchKernelGGL(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)blocks, div, out);
+  if (blocks > 1) rt::launch(sum_stage2, dim3(1), dim3(64), 0, s, scratch, (int)blocks, div, out);
   return hipGetLastError();
 }
 
 hipError_t loss_terms_launch(hipStream_t s, int kind, const float* p, const float* y, float* term, float* dir,
                              long long n) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(loss_terms_kernel, dim3(grid_for(n)), dim3(256), 0, s, kind, p, y, term, dir, n);
+  rt::launch(loss_terms_kernel, dim3(grid_for(n)), dim3(256), 0, s, kind, p, y, term, dir, n);
   return hipGetLastError();
 }
 
