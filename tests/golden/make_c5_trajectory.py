@@ -16,7 +16,16 @@ Its matmul is row-parallel, which is bit-identical to the single-threaded
 one (each element's k order is unchanged), so any thread count gives these
 losses.
 
-Run: python tests/golden/make_c5_trajectory.py [threads]   (~30 s per step on 8)
+The conditioning of that trajectory: the same 100 steps through two
+independent numpy restatements of the bf16 plan's rounding points
+(tests/gpu_common.numpy_bf16_trajectory, float32 and float64 accumulation).
+Early on the loss spikes (7.96 -> 26 -> 13.8 -> 7.3) and the spike amplifies
+step-1 differences ~100x: valid bf16 implementations land several percent
+apart there, so the GPU test bounds each step by max(2e-2, 2 x the farther
+restatement's distance from the oracle).
+
+Run: python tests/golden/make_c5_trajectory.py [threads]        (~30 s per step on 8)
+     python tests/golden/make_c5_trajectory.py --restatements   (adds them, ~45 min)
 """
 import json
 import os
@@ -80,5 +89,24 @@ def main(threads):
     print("wrote", OUT)
 
 
+def restatements():
+    from tests.gpu_common import numpy_bf16_trajectory
+
+    with open(OUT) as f:
+        doc = json.load(f)
+    params = initial_params()
+    for acc in ("f32", "f64"):
+        t0 = time.time()
+        losses = numpy_bf16_trajectory(params, (batch(s) for s in range(STEPS)), LR, acc=acc)
+        doc[f"bf16_restatement_{acc}_acc"] = losses
+        print(f"bf16 restatement, {acc} accumulation: {time.time() - t0:.0f} s", flush=True)
+    with open(OUT, "w") as f:
+        json.dump(doc, f, indent=1)
+    print("wrote", OUT)
+
+
 if __name__ == "__main__":
-    main(int(sys.argv[1]) if len(sys.argv) > 1 else (os.cpu_count() or 1))
+    if len(sys.argv) > 1 and sys.argv[1] == "--restatements":
+        restatements()
+    else:
+        main(int(sys.argv[1]) if len(sys.argv) > 1 else (os.cpu_count() or 1))

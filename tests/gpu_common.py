@@ -288,3 +288,58 @@ def grad_gate(name, want, got, norm_bound, max_bound, erro_bound=None, floor=1e-
         if erro_bound is not None:
             assert r[3] <= erro_bound, f"{name}[{i}]: erro_rel {r[3]:.3e} > {erro_bound:.1e}"
     return rows
+
+
+def numpy_bf16_trajectory(params, batches, lr, loss_scale=1024.0, acc="f32", beta1=0.9, beta2=0.999, eps=1e-8):
+    """The bf16 mixed-precision training step restated in numpy: f32 master
+    weights and Adam (optim.rs:187-195 order), bf16 (round to nearest even)
+    copies of the weights, the inputs, the hidden activations (after ReLU)
+    and δ (after the loss, scaled by loss_scale, and after every ReLU mask),
+    f32 logits and softmax, gradients unscaled by 1/loss_scale.  The GEMMs
+    accumulate in float32 (acc="f32", BLAS order) or float64 (acc="f64") and
+    round to f32: two independent implementations of the plan's rounding
+    points that differ only in accumulation order.  Returns the per-step
+    losses."""
+    from rgpu_amd.gpu import bf16_bits_to_f32, f32_to_bf16_bits
+
+    def rb(a):
+        return bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(a, np.float32)))
+
+    def mm(a, b):
+        if acc == "f64":
+            return (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+        return a @ b
+
+    f = np.float32
+    S = f(loss_scale)
+    ps = [np.asarray(p, np.float32).copy() for p in params]
+    for i in range(1, len(ps), 2):
+        ps[i] = ps[i].reshape(1, -1)
+    m = [np.zeros_like(p) for p in ps]
+    v = [np.zeros_like(p) for p in ps]
+    losses = []
+    for t, (x, lab) in enumerate(batches, start=1):
+        Wh = [rb(W) for W in ps[0::2]]
+        acts = [rb(x)]
+        for l in range(len(Wh)):
+            z = mm(acts[-1], Wh[l]) + ps[2 * l + 1]
+            acts.append(rb(np.maximum(z, f(0))) if l < len(Wh) - 1 else z)
+        z = acts[-1]
+        e = np.exp(z - z.max(1, keepdims=True))
+        p = e / e.sum(1, keepdims=True)
+        B = z.shape[0]
+        losses.append(float(-np.log(np.maximum(p[np.arange(B), lab], f(1e-12))).astype(np.float64).mean()))
+        d = rb((p - np.eye(z.shape[1], dtype=f)[lab]) * f(S / B))
+        g = [None] * len(ps)
+        for l in reversed(range(len(Wh))):
+            g[2 * l] = mm(acts[l].T, d) * f(1 / S)
+            g[2 * l + 1] = d.sum(0, keepdims=True) * f(1 / S)
+            if l > 0:
+                d = rb(mm(d, Wh[l].T) * (acts[l] > 0))
+        c1 = f(1) - f(beta1) ** t
+        c2 = f(1) - f(beta2) ** t
+        for i, gi in enumerate(g):
+            m[i] = m[i] * f(beta1) + gi * (f(1) - f(beta1))
+            v[i] = v[i] * f(beta2) + (gi * gi) * (f(1) - f(beta2))
+            ps[i] -= ((m[i] * (f(1) / c1)) / (np.sqrt(v[i] * (f(1) / c2)) + f(eps))) * f(lr)
+    return losses

@@ -159,10 +159,14 @@ def test_mixed_precision_mlp_full_size_step(gpu):
 def test_mixed_precision_mlp_full_size_100_step_trajectory(gpu):
     """tests/golden/c5_trajectory.json holds the oracle's f32 losses of 100
     Adam steps of the 8 x 4096 -> 1000 MLP at batch 4096 from bf16-rounded
-    weights and inputs (written by make_c5_trajectory.py beside it).  The bf16
-    plan (f32 master weights, loss scale 1024) runs the same 100 steps; every
-    loss must stay within 2e-2 relative of the oracle's (the tests/gpu.rs:
-    99-139 pattern at the bf16 bar)."""
+    weights and inputs (written by make_c5_trajectory.py beside it), and the
+    losses of two independent numpy restatements of the bf16 plan (float32
+    and float64 accumulation).  The bf16 plan (f32 master weights, loss scale
+    1024) runs the same 100 steps; every loss must stay within max(2e-2, 2 x
+    the farther restatement's distance from the oracle at that step) of the
+    oracle's (the tests/gpu.rs:99-139 pattern at the bf16 bar).  The bound
+    exceeds 2e-2 only in the early loss spike (steps 1-3), where valid bf16
+    implementations land several percent apart."""
     import concurrent.futures as cf
     import json
     import os
@@ -171,7 +175,9 @@ def test_mixed_precision_mlp_full_size_100_step_trajectory(gpu):
     with open(os.path.join(os.path.dirname(mk.__file__), "c5_trajectory.json")) as f:
         fix = json.load(f)
     want = [float(np.uint32(b).view(np.float32)) for b in fix["loss_bits"]]
-    assert len(want) == mk.STEPS
+    rest = [fix["bf16_restatement_f32_acc"], fix["bf16_restatement_f64_acc"]]
+    assert len(want) == mk.STEPS and all(len(r) == mk.STEPS for r in rest)
+    bound = [max(2e-2, 2 * max(abs(r[s] - want[s]) / abs(want[s]) for r in rest)) for s in range(mk.STEPS)]
     mlp = G.GpuMlp.from_params(gpu, mk.initial_params(), mk.BATCH, mk.LR, precision="bf16", loss_scale=1024.0)
     t0 = time.time()
     got = []
@@ -182,13 +188,17 @@ def test_mixed_precision_mlp_full_size_100_step_trajectory(gpu):
             mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, lab))
             got.append(mlp.last_loss())
             futs[s] = None
-            if s % 10 == 0:
-                print(f"step {s}: oracle {want[s]:.5f} bf16 {got[-1]:.5f} ({time.time() - t0:.0f} s)", flush=True)
+            if s < 6 or s % 10 == 0:
+                print(f"step {s}: oracle {want[s]:.5f} bf16 {got[-1]:.5f} (restatements {rest[0][s]:.5f}, "
+                      f"{rest[1][s]:.5f}; bound {bound[s]:.1e}) ({time.time() - t0:.0f} s)", flush=True)
     d = [abs(g - w) / abs(w) for g, w in zip(got, want)]
     i = int(np.argmax(d))
-    print(f"100-step trajectory: max rel diff {d[i]:.2e} at step {i} (oracle {want[i]:.5f}, bf16 {got[i]:.5f}); "
-          f"final {want[-1]:.5f} vs {got[-1]:.5f}", flush=True)
-    assert max(d) <= 2e-2
+    late = max(d[10:])
+    print(f"100-step trajectory: max rel diff {d[i]:.2e} at step {i} (bound {bound[i]:.1e}); steps 10-99 "
+          f"{late:.2e}; final {want[-1]:.5f} vs {got[-1]:.5f}", flush=True)
+    for s in range(mk.STEPS):
+        assert d[s] <= bound[s], (s, got[s], want[s], bound[s])
+    assert late <= 2e-2
     assert not mlp.overflow()
 
 
