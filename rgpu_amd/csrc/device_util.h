@@ -49,4 +49,23 @@ __device__ inline void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voff, i
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, voff, so, 0, 0);
 }
 
+// dma16 issued as inline asm.  The compiler orders its own LDS DMA against
+// every later LDS read it cannot prove disjoint with a vmcnt(0) wait, so a
+// pipeline that reads stage k while stage k+1 is in flight waits for stage
+// k+1 before the first read of stage k.  This form is invisible to that
+// bookkeeping: the caller's own wait_vm before its barrier is then the only
+// ordering, and a caller must wait_vm<0>() before reusing the LDS it targets.
+// M0 (the LDS destination) is set inside the asm; kernels that use this form
+// must not also use the builtin, which may keep M0 live across it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ inline void dma16_asm(__amdgpu_buffer_rsrc_t rsrc, void* lds, int voff, int soff) {
+  const int so = __builtin_amdgcn_readfirstlane(soff);
+  const unsigned dst = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(__attribute__((address_space(3))) void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds" ::"s"(dst), "v"(voff), "s"(rsrc),
+               "s"(so)
+               : "m0");
+}
+#pragma clang diagnostic pop
+
 }  // namespace rt_dev
