@@ -639,13 +639,48 @@ __global__ __launch_bounds__(T0::THREADS) void gemm_f32_pair_kernel(F32Args p0, 
   }
 }
 
+// The first cs_blocks blocks each take 256 columns of the column sums: they
+// start first, so their chains of loads run under the plane sums; the rest
+// sum the planes (grid-stride over M*N).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part, int S, long long stride,
                                                              int M, int N, float* C, int ldc, int epi,
                                                              const float* bias, const float* mask,
-                                                             const float* cs_part, float* cs) {
+                                                             const float* __restrict__ cs_part, int cs_rows,
+                                                             float* cs, int cs_blocks) {
+  if ((int)blockIdx.x < cs_blocks) {
+    const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= N) return;
+    // Slice s's column sum: cs_part[s, j], or with shares the cs_rows rows
+    // cs_part[s, t, j] added in order from zero; then the slices in order.
+    // Element e = s * rows + t of that sequence is at cs_part[e * N + j]; the
+    // loads go out 16 at a time and the adds follow in sequence order.
+    const int rows = cs_rows > 0 ? cs_rows : 1;
+    const long long n = (long long)S * rows;
+    float v = 0.0f, w = 0.0f;
+    int t = 0;          // row of element e within its slice
+    bool first = true;  // e lies in slice 0
+    for (long long e0 = 0; e0 < n; e0 += 16) {
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = e0 + u < n ? cs_part[(e0 + u) * N + j] : 0.0f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        if (e0 + u >= n) break;
+        w = cs_rows > 0 ? (t == 0 ? 0.0f : w) + x[u] : x[u];
+        if (++t == rows) {
+          v = first ? w : v + w;
+          first = false;
+          t = 0;
+        }
+      }
+    }
+    cs[j] = v;
+    return;
+  }
+  const int plane_blocks = (int)gridDim.x - cs_blocks;
   const long long total = (long long)M * N;
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
-       i += (long long)gridDim.x * blockDim.x) {
+  for (long long i = (blockIdx.x - cs_blocks) * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)plane_blocks * blockDim.x) {
     // v = plane 0 + plane 1 + ... in slice order; the loads go out 8 at a
     // time so the chain of adds does not wait on one load after another.
     float v = part[i];
@@ -666,21 +701,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
       if (!(mask[(long long)row * ldc + col] > 0.0f)) v = 0.0f;
     }
     C[(long long)row * ldc + col] = v;
-  }
-  if (cs != nullptr) {
-    for (long long j = blockIdx.x * (long long)blockDim.x + threadIdx.x; j < N; j += (long long)gridDim.x * blockDim.x) {
-      float v = cs_part[j];
-      int s = 1;
-      for (; s + 8 <= S; s += 8) {
-        float t[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) t[q] = cs_part[(long long)(s + q) * N + j];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) v += t[q];
-      }
-      for (; s < S; ++s) v += cs_part[(long long)s * N + j];
-      cs[j] = v;
-    }
   }
 }
 
@@ -821,14 +841,15 @@ hipError_t gemm_pair_launch(hipStream_t s, const GemmDesc& d0, const GemmDesc& d
 
 hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M, int N,
                                 void* C, int out_dtype, int ldc, int epi, const float* bias, const void* mask,
-                                int mask_dtype, const float* colsum_partials, float* colsum) {
+                                int mask_dtype, const float* colsum_partials, float* colsum, int cs_rows) {
   if (out_dtype != RT_F32 || mask_dtype != RT_F32) return hipErrorInvalidValue;
   const long long total = (long long)M * N;
   int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
   if (blocks < 1) blocks = 1;
-  rt::launch(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s, partials, splits, stride, M, N,
-                     static_cast<float*>(C), ldc, epi, bias, static_cast<const float*>(mask), colsum_partials,
-                     colsum);
+  const int cs_blocks = colsum != nullptr ? (N + 255) / 256 : 0;
+  rt::launch(splitk_reduce_kernel, dim3(blocks + cs_blocks), dim3(256), 0, s, partials, splits, stride, M, N,
+             static_cast<float*>(C), ldc, epi, bias, static_cast<const float*>(mask), colsum_partials, cs_rows, colsum,
+             cs_blocks);
   return hipGetLastError();
 }
 

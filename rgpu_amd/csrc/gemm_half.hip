@@ -803,7 +803,7 @@ bool dma_addressable(const HalfArgs& a) {
 
 template <int BM, int BN, int WGM, int WGN, bool A_KC, bool B_KC>
 hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16, float* cs_scratch = nullptr,
-                      size_t cs_scratch_elems = 0) {
+                      size_t cs_scratch_elems = 0, bool shares_to_caller = false) {
   set_tiles<BM, BN>(a);
   // Column sums shared over the M tiles when there are several and room.
   a.cs_parts = nullptr;
@@ -817,7 +817,7 @@ hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16, float* c
   else
     rt::launch((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false, kDmaBK, kDmaStages>), grid, block,
                        0, s, a);
-  if (a.cs_parts) {
+  if (a.cs_parts && !(shares_to_caller && splits > 1)) {
     const long long n = (long long)splits * a.N;
     rt::launch(cs_shares_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.cs_parts,
                        a.tiles_m, splits, a.N, a.colsum, a.nf_flag);
@@ -856,32 +856,35 @@ HalfPath pick_path(const HalfArgs& a, int splits, bool overread_ok) {
 
 template <bool A_KC, bool B_KC>
 hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* cs_scratch, size_t cs_elems,
-                       bool overread_ok) {
+                       bool overread_ok, bool shares_to_caller) {
   const HalfPath hp = pick_path<A_KC, B_KC>(a, splits, overread_ok);
   a.n_ragged = hp.dma && a.N % hp.tile != 0;
   if (!hp.dma || splits > 1) a.nf_flag = nullptr;  // gemm_checks_nonfinite says false for these
   switch (hp.tile) {
     case 256:
-      return hp.dma ? launch_dma<256, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
+      return hp.dma ? launch_dma<256, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems,
+                                                             shares_to_caller)
                     : launch_regs<256, 256, 4, 2, A_KC, B_KC>(s, a, splits, bf16);
     case 128:
-      return hp.dma ? launch_dma<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
+      return hp.dma ? launch_dma<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems,
+                                                             shares_to_caller)
                     : launch_regs<128, 128, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
     default:
-      return hp.dma ? launch_dma<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems)
+      return hp.dma ? launch_dma<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems,
+                                                           shares_to_caller)
                     : launch_regs<64, 64, 2, 2, A_KC, B_KC>(s, a, splits, bf16);
   }
 }
 
-// Launches launch_half issues: 2 when the column sums are shared over the M
-// tiles (launch_dma's rule), else 1.
+// M tiles whose column-sum shares launch_half writes per K slice (launch_dma's
+// rule), 0 when the column sums are not shared.
 template <bool A_KC, bool B_KC>
-int half_launches(const HalfArgs& a, int splits, size_t cs_elems, bool have_scratch, bool overread_ok) {
-  if (B_KC || !a.colsum || !have_scratch) return 1;
+int half_share_rows(const HalfArgs& a, int splits, size_t cs_elems, bool have_scratch, bool overread_ok) {
+  if (B_KC || !a.colsum || !have_scratch) return 0;
   const HalfPath hp = pick_path<A_KC, B_KC>(a, splits, overread_ok);
-  if (!hp.dma) return 1;
+  if (!hp.dma) return 0;
   const int tiles_m = (a.M + hp.tile - 1) / hp.tile;
-  return (tiles_m > 1 && (size_t)splits * tiles_m * a.N <= cs_elems) ? 2 : 1;
+  return (tiles_m > 1 && (size_t)splits * tiles_m * a.N <= cs_elems) ? tiles_m : 0;
 }
 
 }  // namespace
@@ -922,9 +925,15 @@ hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
   const HalfArgs a = half_args(d, splits);
   const bool bf16 = d.in_dtype == RT_BF16;
   switch (d.layout) {
-    case RT_NN: return launch_half<true, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
-    case RT_TN: return launch_half<false, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
-    case RT_NT: return launch_half<true, true>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok);
+    case RT_NN:
+      return launch_half<true, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok,
+                                      d.cs_shares_to_caller);
+    case RT_TN:
+      return launch_half<false, false>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok,
+                                       d.cs_shares_to_caller);
+    case RT_NT:
+      return launch_half<true, true>(s, a, splits, bf16, d.cs_scratch, d.cs_scratch_elems, d.overread_ok,
+                                     d.cs_shares_to_caller);
   }
   return hipErrorInvalidValue;
 }
@@ -940,16 +949,25 @@ bool gemm_checks_nonfinite(const GemmDesc& d) {
   return false;
 }
 
-int gemm_launch_count(const GemmDesc& d) {
-  if (d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) return 1;
+static int share_rows(const GemmDesc& d) {
+  if (d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) return 0;
   const int splits = d.splits < 1 ? 1 : d.splits;
   const HalfArgs a = half_args(d, splits);
   const bool have = d.cs_scratch != nullptr;
   switch (d.layout) {
-    case RT_NN: return half_launches<true, false>(a, splits, d.cs_scratch_elems, have, d.overread_ok);
-    case RT_TN: return half_launches<false, false>(a, splits, d.cs_scratch_elems, have, d.overread_ok);
-    default: return 1;
+    case RT_NN: return half_share_rows<true, false>(a, splits, d.cs_scratch_elems, have, d.overread_ok);
+    case RT_TN: return half_share_rows<false, false>(a, splits, d.cs_scratch_elems, have, d.overread_ok);
+    default: return 0;
   }
+}
+
+int gemm_launch_count(const GemmDesc& d) {
+  if (share_rows(d) == 0) return 1;
+  return (d.cs_shares_to_caller && d.splits > 1) ? 1 : 2;  // the shares are added by a second launch
+}
+
+int gemm_cs_share_rows(const GemmDesc& d) {
+  return (d.cs_shares_to_caller && d.splits > 1) ? share_rows(d) : 0;
 }
 
 size_t colsum_scratch_need(int M, int N, int splits) {

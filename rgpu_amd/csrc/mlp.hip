@@ -161,6 +161,7 @@ static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, co
   d.splits = splits;
   d.split_stride = (long long)M * N;
   d.colsum_partials = colsum ? parts + (size_t)splits * M * N : nullptr;
+  d.cs_shares_to_caller = true;  // finish_split adds the column-sum shares
   // Where the reduction puts the result and what it applies.
   d.epi = RT_EPI_NONE;
   return d;
@@ -170,9 +171,11 @@ static int finish_split(rt_mlp* p, const GemmDesc& d, const char* lbl_red, void*
                         const float* bias, const void* mask, int mask_dtype, float* colsum) {
   if (d.splits <= 1) return RT_OK;
   rt_ctx* c = p->ctx;
+  const int cs_rows = gemm_cs_share_rows(d);
   Launch Lz(c, lbl_red);
   hipError_t e = splitk_reduce_launch(c->stream, p->partials, d.splits, d.split_stride, d.M, d.N, C, out_dtype, d.N,
-                                      epi, bias, mask, mask_dtype, d.colsum_partials, colsum);
+                                      epi, bias, mask, mask_dtype, cs_rows ? d.cs_scratch : d.colsum_partials,
+                                      colsum, cs_rows);
   if (e != hipSuccess) return hip_fail(c, e, lbl_red);
   return RT_OK;
 }

@@ -168,6 +168,11 @@ struct GemmDesc {
   // shares in a fixed order (otherwise the first M tile sums all of K alone).
   float* cs_scratch = nullptr;
   size_t cs_scratch_elems = 0;
+  // Split launches (splits > 1) whose column sums go through those shares:
+  // leave the shares, [splits, gemm_cs_share_rows(d), N], in cs_scratch for
+  // the caller's splitk_reduce_launch instead of a second launch that adds
+  // them into colsum_partials.
+  bool cs_shares_to_caller = false;
   // The caller guarantees that A and B may be read up to 1 KiB past their
   // last element (memory inside the same allocation): lets the half GEMM's
   // direct-to-LDS kernel take an N that is not a multiple of its tile.
@@ -178,6 +183,9 @@ struct GemmDesc {
 };
 bool gemm_checks_nonfinite(const GemmDesc& d);
 size_t colsum_scratch_need(int M, int N, int splits);
+// Rows of column-sum shares per K slice that a cs_shares_to_caller launch of
+// d leaves in cs_scratch (0: it writes colsum_partials itself).
+int gemm_cs_share_rows(const GemmDesc& d);
 // Kernel launches gemm_launch issues for d (1, or 2 with shared column sums).
 int gemm_launch_count(const GemmDesc& d);
 
@@ -191,9 +199,14 @@ bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1);
 hipError_t gemm_pair_launch(hipStream_t s, const GemmDesc& d0, const GemmDesc& d1);
 // Sums `splits` f32 partial planes of [M, N] in slice order into C and applies
 // the epilogue; also sums colsum partials [splits, N] into colsum if given.
+// With cs_rows > 0 colsum_partials holds a split half GEMM's column-sum
+// shares [splits, cs_rows, N] instead: each slice's rows are added in order
+// from zero, then the slices in order (the bits of the GEMM's own shares
+// launch followed by the plain reduction).
 hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits, long long stride, int M,
                                 int N, void* C, int out_dtype, int ldc, int epi, const float* bias,
-                                const void* mask, int mask_dtype, const float* colsum_partials, float* colsum);
+                                const void* mask, int mask_dtype, const float* colsum_partials, float* colsum,
+                                int cs_rows = 0);
 
 // ---------------------------------------------------------------- row / column kernels
 hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, int cols, float* dst,

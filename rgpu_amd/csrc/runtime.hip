@@ -602,6 +602,8 @@ int splitk_run(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt
   d.splits = (int)slices;
   d.split_stride = (long long)(M * N);
   d.colsum_partials = colsum ? part + slices * M * N : nullptr;
+  d.cs_shares_to_caller = true;  // the reduction below adds the column-sum shares
+  const int cs_rows = gemm_cs_share_rows(d);
   {
     Launch L(c, "splitk_gemm");
     HIP_TRY(c, gemm_launch(c->stream, d), "split-K gemm");
@@ -609,8 +611,8 @@ int splitk_run(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt
   Launch L(c, "splitk_reduce");
   HIP_TRY(c,
           splitk_reduce_launch(c->stream, part, (int)slices, (long long)(M * N), (int)M, (int)N, out->ptr, RT_F32,
-                               (int)N, RT_EPI_NONE, nullptr, nullptr, RT_F32, d.colsum_partials,
-                               colsum ? static_cast<float*>(colsum->ptr) : nullptr),
+                               (int)N, RT_EPI_NONE, nullptr, nullptr, RT_F32, cs_rows ? d.cs_scratch : d.colsum_partials,
+                               colsum ? static_cast<float*>(colsum->ptr) : nullptr, cs_rows),
           "split-K reduce");
   return RT_OK;
 }
