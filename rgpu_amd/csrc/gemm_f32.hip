@@ -750,8 +750,110 @@ hipError_t launch_dma(hipStream_t s, F32Args a) {
   return hipGetLastError();
 }
 
+// Skinny products: at most 64 rows of output, A K-contiguous (the NN
+// forward and the NT dX of a small batch).  A block owns 16 output columns
+// over the whole K; its 8 waves take consecutive runs of 16-k sub-blocks and
+// issue the loads of up to 8 sub-blocks together ahead of their MFMAs, so
+// the K loop is a few memory round trips instead of one per step.  The
+// waves' partial tiles are added in LDS in wave order, then the epilogue.
+// One launch and no partial planes, where split-K needs a reduction launch.
+//
+// Within a sub-block at k0, lane (g, r) feeds MFMA step q the element
+// k0 + 4g + q of its A row and B column (one float4 of A per sub-block); the
+// accumulator of row block rb holds C[16 rb + 4g + q][n0 + r].
+constexpr int kSkinnyWaves = 8, kSkinnyChunk = 8;
+
+template <int RB, bool B_KC>
+__global__ __launch_bounds__(64 * kSkinnyWaves) void gemm_f32_skinny_kernel(F32Args p) {
+  __shared__ float red[kSkinnyWaves * RB * 16 * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, r = lane & 15;
+  const int n0 = blockIdx.x * 16;
+  const int nsub = p.K / 16;  // K % 16 == 0 (checked by the host)
+  const int per = (nsub + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int s_end = min(nsub, (wave + 1) * per);
+
+  f4 acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sb = wave * per; sb < s_end; sb += kSkinnyChunk) {
+    f4 a[kSkinnyChunk][RB], b[kSkinnyChunk];
+#pragma unroll
+    for (int c = 0; c < kSkinnyChunk; ++c) {
+      const int k = 16 * (sb + c) + 4 * g;
+      const bool in = sb + c < s_end;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int row = 16 * rb + r;
+        a[c][rb] = (in && row < p.M) ? *reinterpret_cast<const f4*>(p.A + (long long)row * p.lda + k)
+                                     : f4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+      if (!in) {
+        b[c] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+      } else if constexpr (B_KC) {
+        b[c] = *reinterpret_cast<const f4*>(p.B + (long long)(n0 + r) * p.ldb + k);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) b[c][q] = p.B[(long long)(k + q) * p.ldb + n0 + r];
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kSkinnyChunk; ++c)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][rb][q], b[c][q], acc[rb], 0, 0, 0);
+  }
+
+  // red[w][row][col]: wave w's partial C[row][n0 + col].
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[(wave * RB * 16 + 16 * rb + 4 * g + q) * 16 + r] = acc[rb][q];
+  __syncthreads();
+  for (int e = tid; e < RB * 16 * 16; e += 64 * kSkinnyWaves) {
+    const int row = e >> 4, col = n0 + (e & 15);
+    if (row >= p.M) continue;
+    float v = red[e];
+#pragma unroll
+    for (int w = 1; w < kSkinnyWaves; ++w) v += red[w * RB * 16 * 16 + e];
+    if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
+      v = v + p.bias[col];
+      if (p.epi == RT_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
+    } else if (p.epi == RT_EPI_RELU_MASK) {
+      if (!(p.mask[(long long)row * p.ldc + col] > 0.0f)) v = 0.0f;
+    }
+    p.C[(long long)row * p.ldc + col] = v;
+  }
+}
+
+// The skinny kernel takes a product when it has at most 64 rows, too few
+// 64x64 tiles to fill the chip, whole 16-column and 16-k blocks, a
+// K-contiguous A (NN or NT) with float4-loadable rows, and no K slices or
+// column sums.
+template <bool A_KC, bool B_KC>
+bool skinny_ok(const F32Args& a) {
+  auto al = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  const long long tiles = (long long)((a.M + 63) / 64) * ((a.N + 63) / 64);
+  return A_KC && a.splits == 1 && a.colsum == nullptr && rt::gemm_f32_skinny_shape(a.M, a.N, a.K) && tiles < 256 &&
+         a.lda % 4 == 0 && al(a.A) && (!B_KC || (a.ldb % 4 == 0 && al(a.B)));
+}
+
+template <bool B_KC>
+hipError_t launch_skinny(hipStream_t s, const F32Args& a) {
+  const dim3 grid(a.N / 16), block(64 * kSkinnyWaves);
+  if (a.M <= 32)
+    rt::launch((gemm_f32_skinny_kernel<2, B_KC>), grid, block, 0, s, a);
+  else
+    rt::launch((gemm_f32_skinny_kernel<4, B_KC>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
 template <bool A_KC, bool B_KC>
 hipError_t dispatch_tile(hipStream_t s, F32Args a) {
+  if constexpr (A_KC) {
+    if (skinny_ok<A_KC, B_KC>(a)) return launch_skinny<B_KC>(s, a);
+  }
   switch (pick_tile(a)) {
     case kT128: return launch_f32<128, 128, A_KC, B_KC>(s, a);
     case kT64x32: return launch_f32<64, 32, A_KC, B_KC>(s, a);
@@ -810,6 +912,10 @@ hipError_t launch_pair_tn_nt(hipStream_t s, F32Args a0, F32Args a1) {
 }  // namespace
 
 namespace rt {
+
+bool gemm_f32_skinny_shape(int M, int N, int K) {
+  return M >= 1 && M <= 64 && N >= 16 && N % 16 == 0 && K >= 128 && K % 16 == 0;
+}
 
 hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d) {
   const F32Args a = make_args(d);

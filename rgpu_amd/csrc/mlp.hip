@@ -372,14 +372,19 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     // batches, the hidden layers' forward and dX too, whose bias+ReLU or
     // ReLU-mask epilogue then runs in the reduction (f32 plans; the bf16
     // plan's hidden outputs are bf16, which the reduction does not write).
-    // The bf16 plan counts its 256x256 tiles instead (half_slices): a
-    // 1000-class head at batch 4096 has 64 of them.
+    // Forward and dX products of at most 64 rows go whole to the skinny f32
+    // kernel instead (one launch, its own epilogue).  The bf16 plan counts
+    // its 256x256 tiles (half_slices): a 1000-class head at batch 4096 has
+    // 64 of them.
     if (p->mixed) {
       Ly.splits_fwd = last ? half_slices(batch, Ly.dout, Ly.din) : 1;
       Ly.splits_dw = half_slices(Ly.din, Ly.dout, batch);
     } else {
-      Ly.splits_fwd = (int)rt_splitk_slices(batch, Ly.dout, Ly.din);
-      Ly.splits_dx = l > 0 ? (int)rt_splitk_slices(batch, Ly.din, Ly.dout) : 1;
+      auto slices = [](size_t m, size_t n, size_t k) {
+        return gemm_f32_skinny_shape((int)m, (int)n, (int)k) ? 1 : (int)rt_splitk_slices(m, n, k);
+      };
+      Ly.splits_fwd = slices(batch, Ly.dout, Ly.din);
+      Ly.splits_dx = l > 0 ? slices(batch, Ly.din, Ly.dout) : 1;
       Ly.splits_dw = (int)rt_splitk_slices(Ly.din, Ly.dout, batch);
     }
     Ly.ldh = (p->mixed && last) ? round_up(Ly.dout, 64) : Ly.dout;
@@ -493,7 +498,10 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     const GemmDesc dx = plan_desc(p, RT_NT, dt, Ly.delta, p->theta + Ly.w_off, p->L[l - 1].delta, RT_F32, (int)batch,
                                   (int)Ly.din, (int)Ly.dout, (int)Ly.dout, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr,
                                   p->L[l - 1].act, RT_F32, nullptr, 1);
-    Ly.pair_bwd = Ly.splits_dx == 1 && gemm_pair_supported(dw, dx);
+    // Not when the dX product runs on the skinny kernel: in the pair its
+    // tiles would walk the whole K alone (batch 32: 41 µs against ~14).
+    const bool skinny_dx = !p->mixed && gemm_f32_skinny_shape((int)batch, (int)Ly.din, (int)Ly.dout);
+    Ly.pair_bwd = Ly.splits_dx == 1 && !skinny_dx && gemm_pair_supported(dw, dx);
   }
 
   const Layer& top = p->L[n_layers - 1];

@@ -192,6 +192,10 @@ int gemm_launch_count(const GemmDesc& d);
 // Enqueues C (or its partial planes) on stream.  Shapes and pointers are
 // validated by the caller.
 hipError_t gemm_launch(hipStream_t s, const GemmDesc& d);
+// The shapes an unsplit f32 NN / NT product of at most 64 rows runs on the
+// skinny kernel (whole K per block, no partial planes) when its operands are
+// float4-aligned: 16-column and 16-k blocks, K >= 128.
+bool gemm_f32_skinny_shape(int M, int N, int K);
 // Two independent GEMMs in one launch: d0 TN (any K slices) and d1 NT
 // (whole K), f32, where both would run on 64x64 tiles.  gemm_pair_supported
 // says whether gemm_pair_launch accepts the pair.

@@ -133,6 +133,40 @@ def test_gemm_epilogues(gpu, m, n, k):
     assert np.all(got[act <= 0] == 0)
 
 
+
+# Products of at most 64 rows with 16-column and 16-k blocks (K >= 128) run on
+# the skinny kernel: 8 waves of a block split K and their partial tiles are
+# added in LDS.  Row counts below, at and above a 16-row block, K runs of one
+# to several load chunks per wave.
+@pytest.mark.parametrize("m,n,k", [(1, 16, 128), (17, 48, 144), (32, 1024, 512), (33, 64, 1040), (64, 512, 1024),
+                                   (64, 16, 4096)])
+def test_skinny_products_with_epilogues(gpu, m, n, k):
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.normal(size=(m, k)).astype(np.float32)
+    w = rng.normal(size=(k, n)).astype(np.float32)
+    bias = rng.normal(size=(1, n)).astype(np.float32)
+    ga, gw, gbias = gpu.upload(a), gpu.upload(w), gpu.upload(bias)
+    exact = a.astype(np.float64) @ w.astype(np.float64) + bias
+    cpu = O.matmul(a, w) + bias
+    c = gpu.zeros((m, n))
+    gpu.matmul_bias(ga, gw, c, gbias, relu=False)
+    assert_near_exact(gpu.download(c), exact, cpu, floor=2e-5, what=f"NN+bias {m}x{n}x{k}")
+    gpu.matmul_bias(ga, gw, c, gbias, relu=True)
+    got = gpu.download(c)
+    assert_near_exact(got, np.maximum(exact, 0), np.maximum(cpu, 0), floor=2e-5, what=f"NN+bias+relu {m}x{n}x{k}")
+    assert (got >= 0).all()
+    # NT with the ReLU mask: out [m, n] = d [m, k] · v [n, k]ᵀ, zero where act <= 0
+    d = rng.normal(size=(m, k)).astype(np.float32)
+    v = rng.normal(size=(n, k)).astype(np.float32)
+    act = np.maximum(rng.normal(size=(m, n)).astype(np.float32), 0)
+    exact = (d.astype(np.float64) @ v.astype(np.float64).T) * (act > 0)
+    cpu = O.matmul(d, v.T.copy()) * (act > 0)
+    out = gpu.zeros((m, n))
+    gpu.matmul_a_bt(gpu.upload(d), gpu.upload(v), out, relu_mask_from=gpu.upload(act))
+    got = gpu.download(out)
+    assert_near_exact(got, exact, cpu, floor=2e-5, what=f"NT+mask {m}x{n}x{k}")
+    assert np.all(got[act <= 0] == 0)
+
 @pytest.mark.parametrize("k,m,n", [(2048, 1024, 10), (64, 130, 96), (513, 64, 1024), (256, 128, 192)])
 def test_tn_gemm_fused_colsum(gpu, k, m, n):
     rng = np.random.default_rng(3)
