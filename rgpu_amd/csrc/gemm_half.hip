@@ -817,7 +817,7 @@ hipError_t launch_dma(hipStream_t s, HalfArgs a, int splits, bool bf16, float* c
   else
     rt::launch((gemm_half_dma_kernel<BM, BN, WGM, WGN, A_KC, B_KC, false, kDmaBK, kDmaStages>), grid, block,
                        0, s, a);
-  if (a.cs_parts && !(shares_to_caller && splits > 1)) {
+  if (a.cs_parts && !shares_to_caller) {
     const long long n = (long long)splits * a.N;
     rt::launch(cs_shares_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a.cs_parts,
                        a.tiles_m, splits, a.N, a.colsum, a.nf_flag);
@@ -963,12 +963,10 @@ static int share_rows(const GemmDesc& d) {
 
 int gemm_launch_count(const GemmDesc& d) {
   if (share_rows(d) == 0) return 1;
-  return (d.cs_shares_to_caller && d.splits > 1) ? 1 : 2;  // the shares are added by a second launch
+  return d.cs_shares_to_caller ? 1 : 2;  // otherwise the shares are added by a second launch
 }
 
-int gemm_cs_share_rows(const GemmDesc& d) {
-  return (d.cs_shares_to_caller && d.splits > 1) ? share_rows(d) : 0;
-}
+int gemm_cs_share_rows(const GemmDesc& d) { return d.cs_shares_to_caller ? share_rows(d) : 0; }
 
 size_t colsum_scratch_need(int M, int N, int splits) {
   // The most M tiles any half kernel uses (64-row tiles), per K slice.

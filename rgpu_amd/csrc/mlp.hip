@@ -14,7 +14,9 @@
 //                            the last layer; δ = ∂L/∂Z
 //   partials                 split-K planes (largest user), reused by every
 //                            split GEMM of the step
-//   cs_scratch               column-sum shares of the half dW GEMMs (mixed)
+//   cs_shares[l]             column-sum shares of layer l's half dW GEMM
+//                            (mixed), kept until the split reduction or the
+//                            non-finite check launch adds them
 //   loss_rows [batch]
 //
 // Step (mod.rs:1399-1467 order): forward GEMMs with bias(+ReLU) epilogues;
@@ -57,6 +59,10 @@ struct Layer {
   // dW / db split-K planes of this layer summed by the optimizer (f32 plans):
   // [splits_dw][din*dout] then [splits_dw][dout], owned by this layer.
   float* dw_parts = nullptr;
+  // Mixed plans: the column-sum shares of this layer's dW launch (its own
+  // region; the split reduction or the non-finite check launch adds them).
+  float* cs_shares = nullptr;
+  size_t cs_share_elems = 0;
   std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx, lbl_dx_red, lbl_bwd;
 };
 
@@ -89,8 +95,6 @@ struct rt_mlp {
   float* v = nullptr;
   void* theta_h = nullptr;  // bf16 copy
   float* partials = nullptr;
-  float* cs_scratch = nullptr;  // column-sum shares of the half dW GEMMs
-  size_t cs_scratch_elems = 0;
   size_t partial_elems = 0;
   float* loss_rows = nullptr;
   // Double-buffered batch slots for rt_mlp_load / rt_mlp_step_loaded: pinned
@@ -142,10 +146,6 @@ static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, co
   d.lda = lda;
   d.ldb = ldb;
   d.ldc = N;
-  if (colsum && in_dtype != RT_F32) {
-    d.cs_scratch = p->cs_scratch;
-    d.cs_scratch_elems = p->cs_scratch_elems;
-  }
   if (splits <= 1) {
     d.C = C;
     d.epi = epi;
@@ -165,6 +165,16 @@ static GemmDesc plan_desc(rt_mlp* p, int layout, int in_dtype, const void* A, co
   // Where the reduction puts the result and what it applies.
   d.epi = RT_EPI_NONE;
   return d;
+}
+
+// A mixed plan's dW launch writes its db shares into the layer's own region
+// and leaves them there: a split launch's reduction adds them (finish_split),
+// the non-finite check launch adds a whole launch's (share jobs).
+static void layer_shares(const Layer& Ly, GemmDesc& d) {
+  if (Ly.cs_shares == nullptr) return;
+  d.cs_scratch = Ly.cs_shares;
+  d.cs_scratch_elems = Ly.cs_share_elems;
+  d.cs_shares_to_caller = true;
 }
 
 static int finish_split(rt_mlp* p, const GemmDesc& d, const char* lbl_red, void* C, int out_dtype, int epi,
@@ -413,11 +423,12 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     }
   }
   p->partial_elems = part;
-  // Column-sum shares of the half dW GEMMs (mixed precision only).
-  size_t cs_elems = 0;
+  // Column-sum shares of the half dW GEMMs (mixed precision only), one
+  // region per layer.
+  std::vector<size_t> cs_elems(n_layers, 0);
   if (p->mixed)
     for (int l = 0; l < n_layers; ++l)
-      cs_elems = std::max(cs_elems, colsum_scratch_need((int)p->L[l].din, (int)p->L[l].dout, p->L[l].splits_dw));
+      cs_elems[l] = colsum_scratch_need((int)p->L[l].din, (int)p->L[l].dout, p->L[l].splits_dw);
 
   // Arena layout.
   const size_t A = 256;
@@ -444,7 +455,9 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   std::vector<size_t> o_dw_part(n_layers, 0);
   for (int l = 0; l < n_layers; ++l)
     if (dw_part_elems[l]) o_dw_part[l] = reserve(dw_part_elems[l] * 4);
-  size_t o_cs = cs_elems ? reserve(cs_elems * 4) : 0;
+  std::vector<size_t> o_cs(n_layers, 0);
+  for (int l = 0; l < n_layers; ++l)
+    if (cs_elems[l]) o_cs[l] = reserve(cs_elems[l] * 4);
   size_t o_loss = reserve(batch * 4);
   size_t o_state = reserve(16 * 4);
 
@@ -467,8 +480,10 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   p->partials = part ? (float*)(p->arena + o_part) : nullptr;
   for (int l = 0; l < n_layers; ++l) p->L[l].dw_parts = dw_part_elems[l] ? (float*)(p->arena + o_dw_part[l]) : nullptr;
   p->loss_rows = (float*)(p->arena + o_loss);
-  p->cs_scratch = cs_elems ? (float*)(p->arena + o_cs) : nullptr;
-  p->cs_scratch_elems = cs_elems;
+  for (int l = 0; l < n_layers; ++l) {
+    p->L[l].cs_shares = cs_elems[l] ? (float*)(p->arena + o_cs[l]) : nullptr;
+    p->L[l].cs_share_elems = cs_elems[l];
+  }
   p->state = (int*)(p->arena + o_state);
 
   // Zero everything (padding and moments must start at 0), then upload θ.
@@ -513,12 +528,13 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     const bool fused = l == n_layers - 1 && p->head_fused;
     n += fused ? 1 : (p->L[l].splits_fwd > 1 ? 2 : 1);
     n += (p->L[l].splits_dw > 1 && !p->L[l].dw_parts) ? 2 : 1;
-    if (p->mixed) {  // the dW GEMM may add the shared column sums in a second launch
+    if (p->mixed) {  // the dW GEMM's shares are added elsewhere: one launch
       const Layer& Ly = p->L[l];
       const void* a_in = l == 0 ? nullptr : p->L[l - 1].act;
-      const GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, a_in, Ly.delta_h, p->grad + Ly.w_off, RT_F32, (int)Ly.din,
-                                    (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.ldh, RT_EPI_NONE, nullptr, nullptr,
-                                    RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
+      GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, a_in, Ly.delta_h, p->grad + Ly.w_off, RT_F32, (int)Ly.din,
+                              (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.ldh, RT_EPI_NONE, nullptr, nullptr, RT_F32,
+                              p->grad + Ly.b_off, Ly.splits_dw);
+      layer_shares(Ly, dw);
       n += gemm_launch_count(dw) - 1;
     }
     if (l > 0 && !p->L[l].pair_bwd) n += p->L[l].splits_dx > 1 ? 2 : 1;
@@ -528,15 +544,19 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   if (p->mixed) {
     n += 1;  // step prologue
     int unchecked = 0;  // layers whose dW GEMM cannot flag non-finite values itself
+    int jobs = 0;       // whole dW launches whose db shares the check launch adds
     for (int l = 0; l < n_layers; ++l) {
       const Layer& Ly = p->L[l];
       GemmDesc dw = plan_desc(p, RT_TN, RT_BF16, l == 0 ? nullptr : p->L[l - 1].act, Ly.delta_h, p->grad + Ly.w_off,
                               RT_F32, (int)Ly.din, (int)Ly.dout, (int)batch, (int)Ly.din, (int)Ly.ldh, RT_EPI_NONE,
                               nullptr, nullptr, RT_F32, p->grad + Ly.b_off, Ly.splits_dw);
+      layer_shares(Ly, dw);
       dw.nf_flag = p->state + 1;
       unchecked += !gemm_checks_nonfinite(dw);
+      jobs += Ly.splits_dw <= 1 && gemm_cs_share_rows(dw) > 0;
     }
-    n += (2 * unchecked + kMaxOptTensors - 1) / kMaxOptTensors;  // separate checks, 24 tensors per launch
+    // Separate checks, 24 tensors and 32 share jobs per launch.
+    n += std::max((jobs + kMaxShareJobs - 1) / kMaxShareJobs, (2 * unchecked + kMaxOptTensors - 1) / kMaxOptTensors);
   }
   p->dispatches = n;
   c->mlps.push_back(p);
@@ -585,6 +605,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
 
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
   std::vector<char> unchecked(nl, 1);
+  std::vector<ShareJob> jobs;
   for (int l = nl - 1; l >= 0; --l) {
     Layer& Ly = p->L[l];
     const void* in = l == 0 ? x->ptr : p->L[l - 1].act;
@@ -596,10 +617,14 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
                             Ly.splits_dw, Ly.dw_parts);
     if (p->mixed) {
       // The overflow flag is set by the GEMM's own epilogue where it can;
-      // the other layers' dW/db go to the separate check below.
+      // the other layers' dW/db go to the separate check below, which also
+      // adds a whole launch's db shares into db.
+      layer_shares(Ly, dw);
       dw.nf_flag = overflow;
       unchecked[l] = !gemm_checks_nonfinite(dw);
       if (unchecked[l]) dw.nf_flag = nullptr;
+      const int rows = dw.splits <= 1 ? gemm_cs_share_rows(dw) : 0;
+      if (rows > 0) jobs.push_back(ShareJob{Ly.cs_shares, p->grad + Ly.b_off, rows, (int)Ly.dout});
     }
     if (l == 0) {
       {
@@ -656,10 +681,14 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       ptrs.push_back(p->grad + p->L[l].b_off);
       ns.push_back(p->L[l].dout);
     }
-    for (size_t i = 0; i < ptrs.size(); i += kMaxOptTensors) {
-      const int k = (int)std::min<size_t>(kMaxOptTensors, ptrs.size() - i);
+    // Launch i checks tensors [24 i, 24 i + 24) and adds jobs [32 i, 32 i + 32).
+    for (size_t i = 0; i * kMaxOptTensors < ptrs.size() || i * kMaxShareJobs < jobs.size(); ++i) {
+      const size_t t0 = std::min(ptrs.size(), i * kMaxOptTensors), j0 = std::min(jobs.size(), i * kMaxShareJobs);
+      const int k = (int)std::min<size_t>(kMaxOptTensors, ptrs.size() - t0);
+      const int nj = (int)std::min<size_t>(kMaxShareJobs, jobs.size() - j0);
       Launch Lz(c, "nonfinite_check");
-      hipError_t e = nonfinite_check_launch(c->stream, ptrs.data() + i, ns.data() + i, k, overflow);
+      hipError_t e = nonfinite_check_launch(c->stream, ptrs.data() + t0, ns.data() + t0, k, overflow,
+                                            jobs.data() + j0, nj);
       if (e != hipSuccess) return hip_fail(c, e, "non-finite check");
     }
   }

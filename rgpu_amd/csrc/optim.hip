@@ -159,13 +159,41 @@ struct NonFiniteArgs {
   long long n[rt::kMaxOptTensors];
   int nt;
   int* flag;
+  rt::ShareJob job[rt::kMaxShareJobs];
+  int job_start[rt::kMaxShareJobs + 1];  // first block of each job, after the check blocks
+  int njobs;
+  int check_blocks;
 };
 
-// Grid-stride over every tensor; any lane that sees a NaN/Inf stores 1.
+// Blocks [0, check_blocks) grid-stride over every tensor; any lane that sees
+// a NaN/Inf stores 1.  The blocks after them take 256 columns of a share job
+// each: the job's rows added in order from zero, 8 loads in flight.
 __global__ __launch_bounds__(256) void nonfinite_kernel(NonFiniteArgs a) {
   bool bad = false;
+  if ((int)blockIdx.x >= a.check_blocks) {
+    const int b = blockIdx.x - a.check_blocks;
+    int j = 0;
+    while (j + 1 < a.njobs && a.job_start[j + 1] <= b) ++j;
+    const rt::ShareJob& J = a.job[j];
+    const int col = (b - a.job_start[j]) * 256 + threadIdx.x;
+    if (col >= J.n) return;
+    const float* q = J.src + col;
+    float v = 0.0f;
+    int t = 0;
+    for (; t + 8 <= J.rows; t += 8) {
+      float w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = q[(long long)(t + u) * J.n];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v += w[u];
+    }
+    for (; t < J.rows; ++t) v += q[(long long)t * J.n];
+    J.dst[col] = v;
+    if (!(fabsf(v) <= 3.402823466e38f)) *a.flag = 1;
+    return;
+  }
   for (int t = 0; t < a.nt; ++t) {
-    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < a.n[t]; i += (long long)gridDim.x * 256) {
+    for (long long i = blockIdx.x * 256LL + threadIdx.x; i < a.n[t]; i += (long long)a.check_blocks * 256) {
       const float v = a.p[t][i];
       bad |= !(fabsf(v) <= 3.402823466e38f);
     }
@@ -230,9 +258,10 @@ hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const Op
   return hipGetLastError();
 }
 
-hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag) {
-  if (nt <= 0) return hipSuccess;
-  if (nt > kMaxOptTensors) return hipErrorInvalidValue;
+hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag,
+                                  const ShareJob* jobs, int njobs) {
+  if (nt <= 0 && njobs <= 0) return hipSuccess;
+  if (nt > kMaxOptTensors || njobs > kMaxShareJobs) return hipErrorInvalidValue;
   NonFiniteArgs a{};
   long long total = 0;
   for (int i = 0; i < nt; ++i) {
@@ -240,9 +269,18 @@ hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const
     a.n[i] = (long long)ns[i];
     total += a.n[i];
   }
-  a.nt = nt;
+  a.nt = nt < 0 ? 0 : nt;
   a.flag = flag;
-  int blocks = (int)std::max<long long>(1, std::min<long long>((total + 255) / 256, 2048));
+  a.check_blocks = total > 0 ? (int)std::min<long long>((total + 255) / 256, 2048) : 0;
+  int blocks = a.check_blocks;
+  a.njobs = njobs < 0 ? 0 : njobs;
+  for (int j = 0; j < a.njobs; ++j) {
+    a.job[j] = jobs[j];
+    a.job_start[j] = blocks - a.check_blocks;
+    blocks += (jobs[j].n + 255) / 256;
+  }
+  a.job_start[a.njobs] = blocks - a.check_blocks;
+  if (blocks == 0) return hipSuccess;
   rt::launch(nonfinite_kernel, dim3(blocks), dim3(256), 0, s, a);
   return hipGetLastError();
 }

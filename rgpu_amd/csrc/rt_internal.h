@@ -168,10 +168,11 @@ struct GemmDesc {
   // shares in a fixed order (otherwise the first M tile sums all of K alone).
   float* cs_scratch = nullptr;
   size_t cs_scratch_elems = 0;
-  // Split launches (splits > 1) whose column sums go through those shares:
-  // leave the shares, [splits, gemm_cs_share_rows(d), N], in cs_scratch for
-  // the caller's splitk_reduce_launch instead of a second launch that adds
-  // them into colsum_partials.
+  // Launches whose column sums go through those shares: leave the shares,
+  // [splits, gemm_cs_share_rows(d), N], in cs_scratch for the caller to add
+  // (splitk_reduce_launch for a split launch, nonfinite_check_launch's share
+  // jobs for a whole one) instead of a second launch that adds them into
+  // colsum (colsum_partials when split).
   bool cs_shares_to_caller = false;
   // The caller guarantees that A and B may be read up to 1 KiB past their
   // last element (memory inside the same allocation): lets the half GEMM's
@@ -273,8 +274,20 @@ struct OptParams {
 hipError_t step_begin_launch(hipStream_t s, int* state);
 constexpr int kMaxOptTensors = 24;
 hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const OptParams& p);
-// Sets *flag = 1 if any of the n floats of any tensor is not finite.
-hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag);
+// Column sums of a whole (unsplit) half GEMM left as shares: dst[j] = the
+// rows src[t * n + j], t = 0 .. rows-1, added in order from zero (what the
+// GEMM's own shares launch computes).
+struct ShareJob {
+  const float* src;
+  float* dst;
+  int rows, n;
+};
+constexpr int kMaxShareJobs = 32;
+// Sets *flag = 1 if any of the n floats of any tensor is not finite; in the
+// same launch, adds the column-sum shares of each job into its dst and flags
+// a non-finite sum the same way.
+hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag,
+                                  const ShareJob* jobs = nullptr, int njobs = 0);
 
 // ---------------------------------------------------------------- tensor ops (tensor_ops.hip)
 hipError_t unary_launch(hipStream_t s, int op, float k, const float* x, float* y, long long n);
