@@ -229,25 +229,120 @@ __device__ inline float load_as_f32<unsigned short>(const unsigned short* p, lon
 template <>
 __device__ inline float load_as_f32<_Float16>(const _Float16* p, long long i) { return (float)p[i]; }
 
+// Column sums (rt_colsum, the reference's COLSUM kernels.rs:182-199), two
+// stages, both reduced inside wavefronts and blocks.
+//
+// Stage 1: a block of 16 waves takes a band of LR*V columns over a chunk of
+// rows.  Lane (ro, cg) of a wave, ro = lane / LR and cg = lane % LR, reads V
+// consecutive columns (16 bytes) of row ro of each of the wave's row groups
+// (RW = 64 / LR rows per group; the 16 waves take the groups in turn, four
+// groups' loads issued together) and accumulates them.  The RW rows of a
+// group are then added across lanes with butterfly shuffles (lanes cg, cg +
+// LR, ...), the 16 waves' sums through LDS in wave order, and the chunk's
+// partial row is written (the result itself for one chunk).
+constexpr int kCsWaves = 16, kCsUnroll = 4;
+
 template <typename T>
-__global__ __launch_bounds__(256) void colsum_stage1(const T* __restrict__ src, int rows, int cols, int chunk,
-                                                     float* __restrict__ out) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= cols) return;
-  const int r0 = blockIdx.y * chunk;
-  const int r1 = min(rows, r0 + chunk);
-  float acc = 0.0f;
-  for (int r = r0; r < r1; ++r) acc += load_as_f32<T>(src, (long long)r * cols + c);
-  out[(long long)blockIdx.y * cols + c] = acc;
+struct ColsumVec {  // 16 bytes of T
+  static constexpr int V = 16 / sizeof(T);
+};
+
+template <typename T>
+__device__ inline void colsum_load(const T* __restrict__ src, long long off, int c, int cols, bool vec,
+                                   float (&x)[ColsumVec<T>::V]) {
+  constexpr int V = ColsumVec<T>::V;
+  if (vec && c + V <= cols) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v w = *reinterpret_cast<const u4v*>(src + off + c);
+    const T* e = reinterpret_cast<const T*>(&w);
+#pragma unroll
+    for (int j = 0; j < V; ++j) x[j] = load_as_f32<T>(e, j);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) x[j] = c + j < cols ? load_as_f32<T>(src, off + c + j) : 0.0f;
+  }
 }
 
-__global__ __launch_bounds__(256) void colsum_stage2(const float* __restrict__ part, int parts, int cols,
-                                                     float* __restrict__ dst) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= cols) return;
+template <typename T>
+__global__ __launch_bounds__(64 * kCsWaves) void colsum_stage1(const T* __restrict__ src, int rows, int cols,
+                                                               int chunk, int lr, bool vec, float* __restrict__ out) {
+  constexpr int V = ColsumVec<T>::V;
+  __shared__ float red[kCsWaves * 64 * V];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rw = 64 / lr, ro = lane / lr, cg = lane % lr;
+  const int c = blockIdx.x * lr * V + cg * V;
+  const int r0 = blockIdx.y * chunk, r1 = min(rows, r0 + chunk);
+  float acc[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) acc[j] = 0.0f;
+  // Row group q covers rows r0 + q*rw .. + rw-1; wave w takes q = w, w + 16, ...
+  const int groups = (r1 - r0 + rw - 1) / rw;
+  for (int q0 = wave; q0 < groups; q0 += kCsWaves * kCsUnroll) {
+    float x[kCsUnroll][V];
+#pragma unroll
+    for (int u = 0; u < kCsUnroll; ++u) {
+      const int r = r0 + (q0 + u * kCsWaves) * rw + ro;
+      if (q0 + u * kCsWaves < groups && r < r1 && c < cols)
+        colsum_load<T>(src, (long long)r * cols, c, cols, vec, x[u]);
+      else
+#pragma unroll
+        for (int j = 0; j < V; ++j) x[u][j] = 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kCsUnroll; ++u)
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] += x[u][j];
+  }
+  // The wave's rw row lanes of each column group, added across lanes.
+  for (int d = lr; d < 64; d <<= 1)
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc[j] += __shfl_xor(acc[j], d);
+  if (ro == 0)
+#pragma unroll
+    for (int j = 0; j < V; ++j) red[(wave * 64 + cg) * V + j] = acc[j];
+  __syncthreads();
+  // Thread t < lr*V finishes column band offset t: the waves in order.
+  const int t = threadIdx.x;
+  if (t < lr * V) {
+    const int col = blockIdx.x * lr * V + t;
+    if (col < cols) {
+      const int g = t / V, j = t % V;
+      float v = red[g * V + j];
+      for (int w = 1; w < kCsWaves; ++w) v += red[(w * 64 + g) * V + j];
+      out[(long long)blockIdx.y * cols + col] = v;
+    }
+  }
+}
+
+// Stage 2: dst[col] = the partial rows of the chunks added up.  A block
+// takes 64 columns; wave w adds the parts w, w + 16, ... of its lane's
+// column (four loads in flight), the 16 waves' sums are added in LDS in
+// wave order.
+__global__ __launch_bounds__(64 * kCsWaves) void colsum_stage2(const float* __restrict__ part, int parts, int cols,
+                                                               float* __restrict__ dst) {
+  __shared__ float red[kCsWaves * 64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = blockIdx.x * 64 + lane;
   float acc = 0.0f;
-  for (int s = 0; s < parts; ++s) acc += part[(long long)s * cols + c];
-  dst[c] = acc;
+  if (col < cols) {
+    for (int p0 = wave; p0 < parts; p0 += kCsWaves * kCsUnroll) {
+      float x[kCsUnroll];
+#pragma unroll
+      for (int u = 0; u < kCsUnroll; ++u) {
+        const int p = p0 + u * kCsWaves;
+        x[u] = p < parts ? part[(long long)p * cols + col] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < kCsUnroll; ++u) acc += x[u];
+    }
+  }
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave == 0 && col < cols) {
+    float v = red[lane];
+    for (int w = 1; w < kCsWaves; ++w) v += red[w * 64 + lane];
+    dst[col] = v;
+  }
 }
 
 __global__ __launch_bounds__(256) void bias_add_kernel(float* z, const float* b, int rows, int cols) {
@@ -325,45 +420,60 @@ hipError_t xent_launch(hipStream_t s, const float* logits, const uint32_t* label
   return hipGetLastError();
 }
 
-// Rows per stage-1 chunk: enough chunks that the column blocks times chunks
-// give ~2048 workgroups, but at least 8 rows each.
-static int colsum_chunk(int rows, int cols) {
-  const int cblocks = (cols + 255) / 256;
-  int want = std::max(1, 2048 / cblocks);
-  int chunk = (rows + want - 1) / want;
-  return std::max(chunk, 8);
+// Column sums: lanes per row LR (a power of two covering the columns at 16
+// bytes a lane, at most 64), bands of LR*V columns, and row chunks: about 512
+// blocks over the bands, at least one unrolled round of row groups each.
+struct ColsumPlan {
+  int lr, bands, chunk, parts;
+};
+static ColsumPlan colsum_plan(int rows, int cols, int esize) {
+  const int V = 16 / esize;
+  int lr = 1;
+  while (lr < 64 && lr * V < cols) lr *= 2;
+  const int bands = (cols + lr * V - 1) / (lr * V);
+  const int rw = 64 / lr;
+  const int min_rows = rw * kCsWaves * kCsUnroll;
+  int chunks = std::max(1, 512 / bands);
+  chunks = std::min(chunks, std::max(1, (rows + min_rows - 1) / min_rows));
+  const int chunk = (rows + chunks - 1) / chunks;
+  return ColsumPlan{lr, bands, chunk, (rows + chunk - 1) / chunk};
 }
 
-size_t colsum_scratch_elems(int rows, int cols) {
+static int dtype_bytes(int dtype) { return dtype == RT_F32 ? 4 : 2; }
+
+size_t colsum_scratch_elems(int rows, int cols, int dtype) {
   if (rows <= 0 || cols <= 0) return 0;
-  const int chunk = colsum_chunk(rows, cols);
-  const int parts = (rows + chunk - 1) / chunk;
-  return parts > 1 ? (size_t)parts * cols : 0;
+  const ColsumPlan cp = colsum_plan(rows, cols, dtype_bytes(dtype));
+  return cp.parts > 1 ? (size_t)cp.parts * cols : 0;
 }
 
 hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, int cols, float* dst, float* scratch,
                          size_t scratch_elems) {
   if (cols <= 0) return hipSuccess;
+  const dim3 block(64 * kCsWaves);
   if (rows <= 0) {
-    rt::launch(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, (const float*)nullptr, 0, cols, dst);
+    rt::launch(colsum_stage2, dim3((cols + 63) / 64), block, 0, s, (const float*)nullptr, 0, cols, dst);
     return hipGetLastError();
   }
-  const int chunk = colsum_chunk(rows, cols);
-  const int parts = (rows + chunk - 1) / chunk;
-  float* out1 = parts > 1 ? scratch : dst;
-  if (parts > 1 && (scratch == nullptr || scratch_elems < (size_t)parts * cols)) return hipErrorInvalidValue;
-  dim3 g1((cols + 255) / 256, parts);
+  const int esize = dtype_bytes(dtype);
+  const ColsumPlan cp = colsum_plan(rows, cols, esize);
+  float* out1 = cp.parts > 1 ? scratch : dst;
+  if (cp.parts > 1 && (scratch == nullptr || scratch_elems < (size_t)cp.parts * cols)) return hipErrorInvalidValue;
+  // 16-byte loads when every row starts 16-byte aligned.
+  const bool vec = (reinterpret_cast<uintptr_t>(src) & 15) == 0 && ((size_t)cols * esize) % 16 == 0;
+  const dim3 g1(cp.bands, cp.parts);
   if (dtype == RT_F32)
-    rt::launch(colsum_stage1<float>, g1, dim3(256), 0, s, static_cast<const float*>(src), rows, cols, chunk, out1);
+    rt::launch(colsum_stage1<float>, g1, block, 0, s, static_cast<const float*>(src), rows, cols, cp.chunk, cp.lr,
+               vec, out1);
   else if (dtype == RT_BF16)
-    rt::launch(colsum_stage1<unsigned short>, g1, dim3(256), 0, s, static_cast<const unsigned short*>(src),
-                       rows, cols, chunk, out1);
+    rt::launch(colsum_stage1<unsigned short>, g1, block, 0, s, static_cast<const unsigned short*>(src), rows, cols,
+               cp.chunk, cp.lr, vec, out1);
   else
-    rt::launch(colsum_stage1<_Float16>, g1, dim3(256), 0, s, static_cast<const _Float16*>(src), rows, cols,
-                       chunk, out1);
+    rt::launch(colsum_stage1<_Float16>, g1, block, 0, s, static_cast<const _Float16*>(src), rows, cols, cp.chunk,
+               cp.lr, vec, out1);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || parts == 1) return e;
-  rt::launch(colsum_stage2, dim3((cols + 255) / 256), dim3(256), 0, s, scratch, parts, cols, dst);
+  if (e != hipSuccess || cp.parts == 1) return e;
+  rt::launch(colsum_stage2, dim3((cols + 63) / 64), block, 0, s, scratch, cp.parts, cols, dst);
   return hipGetLastError();
 }
 

@@ -216,7 +216,7 @@ hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits
 // ---------------------------------------------------------------- row / column kernels
 hipError_t colsum_launch(hipStream_t s, const void* src, int dtype, int rows, int cols, float* dst,
                          float* scratch, size_t scratch_elems);
-size_t colsum_scratch_elems(int rows, int cols);
+size_t colsum_scratch_elems(int rows, int cols, int dtype);
 hipError_t bias_add_launch(hipStream_t s, float* z, const float* b, int rows, int cols);
 hipError_t relu_launch(hipStream_t s, const float* x, float* y, size_t n);
 hipError_t relu_bwd_launch(hipStream_t s, const void* a, int a_dtype, float* delta, size_t n);

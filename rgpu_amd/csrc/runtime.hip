@@ -646,7 +646,7 @@ int rt_colsum(rt_ctx* c, const rt_buf* src, rt_buf* dst) {
   size_t R = src->shape[0], Cc = src->shape[1];
   if (dst->dtype != RT_F32 || dst->n != Cc) return fail(c, RT_ERR_SHAPE, "colsum target must be f32 [1,%zu]", Cc);
   if (src->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "colsum of u32");
-  int rc = ensure_scratch(c, colsum_scratch_elems((int)R, (int)Cc));
+  int rc = ensure_scratch(c, colsum_scratch_elems((int)R, (int)Cc, src->dtype));
   if (rc) return rc;
   Launch L(c, "colsum");
   HIP_TRY(c, colsum_launch(c->stream, src->ptr, src->dtype, (int)R, (int)Cc, static_cast<float*>(dst->ptr), c->scratch,
