@@ -284,6 +284,33 @@ def bench_splitk(gpu, G, reps=50, slices=64):
             "frac": round(gbs / PEAK_HBM_GBS, 4), "tflops": round(flops / (t * 1e-3) / 1e12, 1)}
 
 
+def bench_colsum(gpu, G, reps=50):
+    """The bias gradient on its own (rt_colsum, the reference's COLSUM):
+    db = colsum(dY) for the Linear 4096 backward's dY (bf16 [8192, 4096]) and
+    the split-K dW's dY (f16 [262144, 512]), against the HBM roofline."""
+    out = {"config": "db = colsum(dY), f32 out; dY bf16 [8192,4096] ~N(0,1)/64 and f16 [262144,512] ~N(0,1)/16",
+           "bound": "hbm", "peak_gbs": PEAK_HBM_GBS}
+    rng = np.random.default_rng(5)
+    for name, rows, cols, dt, scale in (("bf16_8192x4096", 8192, 4096, G.BF16, 64.0),
+                                        ("f16_262144x512", 262144, 512, G.F16, 16.0)):
+        a = gpu.upload(rng.standard_normal((rows, cols), dtype=np.float32) / np.float32(scale), dt)
+        d = gpu.zeros((1, cols))
+        for _ in range(100):  # past the clock ramp
+            gpu.colsum(a, d)
+        gpu.sync()
+        ts = []
+        for _ in range(5):
+            gpu.timer_begin()
+            for _ in range(reps):
+                gpu.colsum(a, d)
+            ts.append(gpu.timer_end() / reps)
+        t = float(np.median(ts))
+        bytes_ = rows * cols * 2 + cols * 4  # compulsory: read dY, write db
+        gbs = bytes_ / (t * 1e-3) / 1e9
+        out[name] = {"us": round(t * 1e3, 2), "achieved_gbs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+    return out
+
+
 def bench_mixed(gpu, G, steps=20, warmup=10):
     """8 x 4096 ReLU layers -> 1000 classes, batch 4096, bf16 + f32 master, Adam."""
     dims = [4096] * 9 + [1000]
@@ -550,6 +577,21 @@ def cpu_splitk_baseline(rows=16384):
             "sample": f"{rows} of the 262144 rows on the oracle, 1 thread, {s:.2f} s scaled x{K // rows}"}
 
 
+def cpu_colsum_baseline(rows=32768):
+    """reduce_to(dY, (1, 512)) on the oracle over `rows` of the 262144 rows
+    (f32; the CPU path has no f16), 1 thread, scaled by 262144 / rows."""
+    from oracle import oracle as O
+
+    O.set_threads(1)
+    K, N = 262144, 512
+    dy = np.random.default_rng(5).standard_normal((rows, N), dtype=np.float32) / np.float32(16.0)
+    t0 = time.perf_counter()
+    O.reduce_to(dy, (1, N))
+    s = time.perf_counter() - t0
+    return {"value": round(s * K / rows * 1e3, 2), "unit": "ms per db of [262144, 512]", "cores": 1, "kind": "port",
+            "sample": f"{rows} of the 262144 rows on the oracle, 1 thread, {s:.3f} s scaled x{K // rows}"}
+
+
 def cpu_mixed_baseline(batches=(16, 48)):
     """One training step of the 8 x 4096 -> 1000 MLP on the oracle (f32, the
     CPU path has no bf16), 1 thread, at two small batches; the step time is
@@ -619,7 +661,8 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["all", "step", "small", "bwd", "splitk", "mixed", "copy", "tape", "pcie"],
+    ap.add_argument("--only", choices=["all", "step", "small", "bwd", "splitk", "colsum", "mixed", "copy", "tape",
+                                       "pcie"],
                     default="all",
                     help="restrict the GPU work (for profiler passes); the JSON line needs 'all' or 'step'")
     ap.add_argument("--rounds", type=int, default=20,
@@ -634,9 +677,9 @@ def main():
     from rgpu_amd import gpu as G
 
     gpu = G.Gpu(0)
-    if args.only in ("small", "bwd", "splitk", "mixed", "copy", "tape", "pcie"):
-        fn = {"small": bench_small, "bwd": bench_bwd_gemm, "splitk": bench_splitk, "mixed": bench_mixed,
-              "copy": bench_copy, "tape": bench_tape, "pcie": bench_pcie}[args.only]
+    if args.only in ("small", "bwd", "splitk", "colsum", "mixed", "copy", "tape", "pcie"):
+        fn = {"small": bench_small, "bwd": bench_bwd_gemm, "splitk": bench_splitk, "colsum": bench_colsum,
+              "mixed": bench_mixed, "copy": bench_copy, "tape": bench_tape, "pcie": bench_pcie}[args.only]
         res = fn(gpu, G, rounds=args.rounds) if args.only == "bwd" else fn(gpu, G)
         print(json.dumps({args.only: res}), flush=True)
         return
@@ -694,6 +737,7 @@ def main():
         out["small_batch"] = bench_small(gpu, G)
         out["bwd_gemm"] = bench_bwd_gemm(gpu, G)
         out["splitk_dw"] = bench_splitk(gpu, G)
+        out["colsum"] = bench_colsum(gpu, G)
         out["mixed_mlp"] = bench_mixed(gpu, G)
         out["tape_mlp"] = bench_tape(gpu, G)
         out["pcie_inclusive"] = bench_pcie(gpu, G)
@@ -718,6 +762,10 @@ def main():
             c = cpu_splitk_baseline()
             out["splitk_dw"]["cpu_baseline"] = c
             out["splitk_dw"]["speedup_vs_cpu"] = round(c["value"] / out["splitk_dw"]["ms"], 1)
+        if "colsum" in out:
+            c = cpu_colsum_baseline()
+            out["colsum"]["cpu_baseline"] = c
+            out["colsum"]["speedup_vs_cpu"] = round(c["value"] / (out["colsum"]["f16_262144x512"]["us"] * 1e-3), 1)
         if "mixed_mlp" in out:
             c = cpu_mixed_baseline()
             out["mixed_mlp"]["cpu_baseline"] = c
