@@ -705,14 +705,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) void gemm_half_dma_kernel(HalfArgs 
       wait_vm<0>();
       barrier_lds();
       // (k+1, kk 0) fragments (discarded after the last stage) and the DMA of
-      // stage k+2 touch different buffers; with a transposed operand the
-      // fragment reads go first (measured faster), else the DMA.
+      // stage k+2 touch different buffers.  The DMA has one stage of MFMAs
+      // to land, so it starts right after the barrier: NT issues all of it
+      // first; with a transposed operand A's half goes first, then the
+      // fragment reads, then B's half (measured fastest of the orders tried:
+      // reads first, DMA first, and the B-first mirror).
+      const int next = min(k + 2, nk - 1);
       if constexpr (A_KC && B_KC) {
-        issue(min(k + 2, nk - 1), BUF);
+        issue(next, BUF);
         read_frags(BUF ^ 1, 0, fa0, fb0);
       } else {
+        oa.template issue<ASM_DMA>(next * a_step, sA(BUF), wave);
         read_frags(BUF ^ 1, 0, fa0, fb0);
-        issue(min(k + 2, nk - 1), BUF);
+        ob.template issue<ASM_DMA>(next * b_step, sB(BUF), wave);
       }
       mfmas(fa1, fb1);
       interleave(std::integral_constant<int, PER_STAGE>{});
