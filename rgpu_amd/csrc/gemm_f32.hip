@@ -646,7 +646,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                                                              int M, int N, float* C, int ldc, int epi,
                                                              const float* bias, const float* mask,
                                                              const float* __restrict__ cs_part, int cs_rows,
-                                                             float* cs, int cs_blocks) {
+                                                             float* cs, int cs_blocks, int vec4) {
   if ((int)blockIdx.x < cs_blocks) {
     const long long j = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (j >= N) return;
@@ -679,10 +679,52 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
   const int plane_blocks = (int)gridDim.x - cs_blocks;
   const long long total = (long long)M * N;
-  for (long long i = (blockIdx.x - cs_blocks) * (long long)blockDim.x + threadIdx.x; i < total;
-       i += (long long)plane_blocks * blockDim.x) {
+  const long long first = (blockIdx.x - cs_blocks) * (long long)blockDim.x + threadIdx.x;
+  const long long step = (long long)plane_blocks * blockDim.x;
+  if (vec4) {
+    // Four consecutive elements of one row per thread (N, ldc, stride and
+    // every pointer 16-byte aligned); each element's sum is the scalar one.
+    const f4* P = reinterpret_cast<const f4*>(part);
+    const long long s4 = stride / 4, total4 = total / 4;
+    for (long long i = first; i < total4; i += step) {
+      f4 v = P[i];
+      int s = 1;
+      for (; s + 8 <= S; s += 8) {
+        f4 t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = P[(long long)(s + j) * s4 + i];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v += t[j];
+      }
+      f4 t[7];
+#pragma unroll
+      for (int j = 0; j < 7; ++j) t[j] = s + j < S ? P[(long long)(s + j) * s4 + i] : f4{0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 7; ++j)
+        if (s + j < S) v += t[j];
+      const long long e = 4 * i, row = e / N;
+      const int col = (int)(e - row * N);
+      if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) {
+        const f4 b = *reinterpret_cast<const f4*>(bias + col);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          v[q] = v[q] + b[q];
+          if (epi == RT_EPI_BIAS_RELU) v[q] = fmaxf(v[q], 0.0f);
+        }
+      } else if (epi == RT_EPI_RELU_MASK) {
+        const f4 mk = *reinterpret_cast<const f4*>(mask + row * ldc + col);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (!(mk[q] > 0.0f)) v[q] = 0.0f;
+      }
+      *reinterpret_cast<f4*>(C + row * ldc + col) = v;
+    }
+    return;
+  }
+  for (long long i = first; i < total; i += step) {
     // v = plane 0 + plane 1 + ... in slice order; the loads go out 8 at a
-    // time so the chain of adds does not wait on one load after another.
+    // time (the last S - 1 mod 8 together) so the chain of adds does not
+    // wait on one load after another.
     float v = part[i];
     int s = 1;
     for (; s + 8 <= S; s += 8) {
@@ -692,15 +734,25 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 #pragma unroll
       for (int j = 0; j < 8; ++j) v += t[j];
     }
-    for (; s < S; ++s) v += part[(long long)s * stride + i];
-    const int row = (int)(i / N), col = (int)(i % N);
-    if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) {
-      v = v + bias[col];
-      if (epi == RT_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
-    } else if (epi == RT_EPI_RELU_MASK) {
-      if (!(mask[(long long)row * ldc + col] > 0.0f)) v = 0.0f;
+    float t[7];
+#pragma unroll
+    for (int j = 0; j < 7; ++j) t[j] = s + j < S ? part[(long long)(s + j) * stride + i] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 7; ++j)
+      if (s + j < S) v += t[j];
+    long long o = i;  // offset in C
+    if (epi != RT_EPI_NONE || ldc != N) {
+      const long long row = i / N;
+      const int col = (int)(i - row * N);
+      o = row * ldc + col;
+      if (epi == RT_EPI_BIAS || epi == RT_EPI_BIAS_RELU) {
+        v = v + bias[col];
+        if (epi == RT_EPI_BIAS_RELU) v = fmaxf(v, 0.0f);
+      } else if (epi == RT_EPI_RELU_MASK) {
+        if (!(mask[o] > 0.0f)) v = 0.0f;
+      }
     }
-    C[(long long)row * ldc + col] = v;
+    C[o] = v;
   }
 }
 
@@ -950,12 +1002,16 @@ hipError_t splitk_reduce_launch(hipStream_t s, const float* partials, int splits
                                 int mask_dtype, const float* colsum_partials, float* colsum, int cs_rows) {
   if (out_dtype != RT_F32 || mask_dtype != RT_F32) return hipErrorInvalidValue;
   const long long total = (long long)M * N;
-  int blocks = (int)std::min<long long>((total + 255) / 256, 4096);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec4 = N % 4 == 0 && ldc % 4 == 0 && stride % 4 == 0 && al16(partials) && al16(C) &&
+                    (bias == nullptr || al16(bias)) && (mask == nullptr || al16(mask));
+  const long long items = vec4 ? total / 4 : total;
+  int blocks = (int)std::min<long long>((items + 255) / 256, 4096);
   if (blocks < 1) blocks = 1;
   const int cs_blocks = colsum != nullptr ? (N + 255) / 256 : 0;
   rt::launch(splitk_reduce_kernel, dim3(blocks + cs_blocks), dim3(256), 0, s, partials, splits, stride, M, N,
              static_cast<float*>(C), ldc, epi, bias, static_cast<const float*>(mask), colsum_partials, cs_rows, colsum,
-             cs_blocks);
+             cs_blocks, vec4 ? 1 : 0);
   return hipGetLastError();
 }
 
