@@ -304,6 +304,26 @@ def test_adam_and_sgd_are_bit_exact_with_cpu_arithmetic(gpu):
     assert np.array_equal(gpu.download(gt2), p2.value())
 
 
+def test_adam_launch_larger_than_the_cache_gives_the_same_bits(gpu):
+    # An optimizer launch that moves more than the 256 MB last-level cache
+    # reads and writes its streams non-temporally; the same update as two
+    # launches of half the size each does not.  Same arithmetic, same bits.
+    n, h = 10_000_000, 5_000_000  # 28 B per Adam parameter: ~280 MB, ~140 MB
+    rng = np.random.default_rng(21)
+    theta = rng.normal(size=(1, n)).astype(np.float32)
+    whole = [gpu.upload(theta), gpu.zeros((1, n)), gpu.zeros((1, n))]
+    parts = [[gpu.upload(np.ascontiguousarray(theta[:, s])), gpu.zeros((1, h)), gpu.zeros((1, h))]
+             for s in (slice(0, h), slice(h, n))]
+    for t in (1, 2, 3):
+        g = (rng.normal(size=(1, n)) * 10.0 ** -t).astype(np.float32)
+        gpu.adam(*whole, gpu.upload(g), 1e-3, (0.9, 0.999), t)
+        for (th, m, v), s in zip(parts, (slice(0, h), slice(h, n))):
+            gpu.adam(th, m, v, gpu.upload(np.ascontiguousarray(g[:, s])), 1e-3, (0.9, 0.999), t)
+    for i in range(3):  # theta, m, v
+        want = np.concatenate([gpu.download(parts[0][i]), gpu.download(parts[1][i])], axis=1)
+        assert np.array_equal(gpu.download(whole[i]), want), i
+
+
 @pytest.mark.parametrize("m,n,k", [(64, 64, 64), (256, 128, 512), (512, 512, 256), (130, 70, 200)])
 @pytest.mark.parametrize("dt", [G.F16, G.BF16])
 def test_half_gemm_three_layouts(gpu, m, n, k, dt):  # gpu.rs:445-503
