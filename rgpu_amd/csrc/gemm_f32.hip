@@ -615,6 +615,69 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_kernel(F32Args p) {
   T::run(p, xcd_local(blockIdx.x, gridDim.x), blockIdx.z, smem);
 }
 
+// C = A·Bᵀ (NT) for K <= 16, one 64x64 block of C per workgroup: the
+// block's 64 rows of A and 64 rows of B go to LDS, and thread t computes
+// rows 4(t/16) .. +3, columns 4(t%16) .. +3 with K multiply-adds each, in k
+// order, then applies the epilogue.  A rank-K update is a stream of C (and
+// of the mask): the MFMA tile's K pipeline padded to 32 only adds latency.
+struct F32RankK {
+  static constexpr int THREADS = 256;
+  static constexpr int KMAX = 16;
+  static constexpr int LD = KMAX + 1;  // LDS row stride (floats)
+  static constexpr int SMEM = 2 * 64 * LD;
+  __device__ static void run(const F32Args& p, int bid, int, float* smem) {
+    float* sa = smem;
+    float* sb = smem + 64 * LD;
+    const int tile_m = bid / p.tiles_n, tile_n = bid - tile_m * p.tiles_n;
+    const int m0 = 64 * tile_m, n0 = 64 * tile_n, K = p.K, tid = threadIdx.x;
+    for (int i = tid; i < 64 * K; i += THREADS) {
+      const int r = i / K, k = i - r * K;
+      sa[r * LD + k] = m0 + r < p.M ? p.A[(long long)(m0 + r) * p.lda + k] : 0.0f;
+      sb[r * LD + k] = n0 + r < p.N ? p.B[(long long)(n0 + r) * p.ldb + k] : 0.0f;
+    }
+    __syncthreads();
+    const int r0 = 4 * (tid / 16), c0 = 4 * (tid % 16);
+    f4 acc[4] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}, f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
+    for (int k = 0; k < K; ++k) {
+      const f4 b = f4{sb[c0 * LD + k], sb[(c0 + 1) * LD + k], sb[(c0 + 2) * LD + k], sb[(c0 + 3) * LD + k]};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] += sa[(r0 + i) * LD + k] * b;
+    }
+    const int col = n0 + c0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = m0 + r0 + i;
+      if (row >= p.M) break;
+      f4 v = acc[i];
+      float* c = p.C + (long long)row * p.ldc + col;
+      const float* mk = p.mask + (long long)row * p.ldc + col;
+      if (p.vec_c && col + 4 <= p.N) {
+        if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
+          v += *reinterpret_cast<const f4*>(p.bias + col);
+          if (p.epi == RT_EPI_BIAS_RELU)
+            for (int q = 0; q < 4; ++q) v[q] = fmaxf(v[q], 0.0f);
+        } else if (p.epi == RT_EPI_RELU_MASK) {
+          const f4 m = *reinterpret_cast<const f4*>(mk);
+          for (int q = 0; q < 4; ++q)
+            if (!(m[q] > 0.0f)) v[q] = 0.0f;
+        }
+        *reinterpret_cast<f4*>(c) = v;
+      } else {
+        for (int q = 0; q < 4 && col + q < p.N; ++q) {
+          float x = v[q];
+          if (p.epi == RT_EPI_BIAS || p.epi == RT_EPI_BIAS_RELU) {
+            x = x + p.bias[col + q];
+            if (p.epi == RT_EPI_BIAS_RELU) x = fmaxf(x, 0.0f);
+          } else if (p.epi == RT_EPI_RELU_MASK && !(mk[q] > 0.0f)) {
+            x = 0.0f;
+          }
+          c[q] = x;
+        }
+      }
+    }
+  }
+};
+
 // Two independent GEMMs in one launch (horizontal fusion): blocks
 // [0, n0) run problem 0, the rest problem 1, each problem's split index
 // folded into its block range.  n0 is a multiple of 8 so both problems are
@@ -901,10 +964,28 @@ hipError_t launch_skinny(hipStream_t s, const F32Args& a) {
   return hipGetLastError();
 }
 
+// dX of a narrow layer (K = that layer's outputs <= 16): the rank-K block.
+bool rank_k_ok(const F32Args& a) {
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool epi_ok = (a.epi != RT_EPI_RELU_MASK || al16(a.mask)) &&
+                      ((a.epi != RT_EPI_BIAS && a.epi != RT_EPI_BIAS_RELU) || al16(a.bias));
+  return a.K >= 1 && a.K <= F32RankK::KMAX && a.splits <= 1 && epi_ok;
+}
+
+hipError_t launch_rank_k(hipStream_t s, F32Args a) {
+  a.tiles_m = (a.M + 63) / 64;
+  a.tiles_n = (a.N + 63) / 64;
+  rt::launch((gemm_f32_kernel<F32RankK>), dim3(a.tiles_m * a.tiles_n), dim3(F32RankK::THREADS), 0, s, a);
+  return hipGetLastError();
+}
+
 template <bool A_KC, bool B_KC>
 hipError_t dispatch_tile(hipStream_t s, F32Args a) {
   if constexpr (A_KC) {
     if (skinny_ok<A_KC, B_KC>(a)) return launch_skinny<B_KC>(s, a);
+  }
+  if constexpr (A_KC && B_KC) {
+    if (rank_k_ok(a)) return launch_rank_k(s, a);
   }
   switch (pick_tile(a)) {
     case kT128: return launch_f32<128, 128, A_KC, B_KC>(s, a);
@@ -984,14 +1065,20 @@ bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1) {
   if (d0.layout != RT_TN || d1.layout != RT_NT || d1.splits > 1) return false;
   // Only where the single launches would use the same tiles.
   const TileCfg t0 = pick_tile(make_args(d0));
-  return (t0 == kT64 || t0 == kT64x32) && pick_tile(make_args(d1)) == kT64;
+  return (t0 == kT64 || t0 == kT64x32) && (pick_tile(make_args(d1)) == kT64 || rank_k_ok(make_args(d1)));
 }
 
 hipError_t gemm_pair_launch(hipStream_t s, const GemmDesc& d0, const GemmDesc& d1) {
   if (!gemm_pair_supported(d0, d1)) return hipErrorInvalidValue;
   const F32Args a0 = make_args(d0), a1 = make_args(d1);
+  // dX takes the block its single launch would (the rank-K block for K <= 16).
+  const bool rk = rank_k_ok(a1);
   if (pick_tile(a0) == kT64x32)
-    return launch_pair_tn_nt<F32Tile<64, 32, false, false>, F32Tile<64, 64, true, true>, 32>(s, a0, a1);
+    return rk ? launch_pair_tn_nt<F32Tile<64, 32, false, false>, F32RankK, 32>(s, a0, a1)
+              : launch_pair_tn_nt<F32Tile<64, 32, false, false>, F32Tile<64, 64, true, true>, 32>(s, a0, a1);
+  if (rk)
+    return dma_ok<false, false>(a0) ? launch_pair_tn_nt<F32DmaTile<false, false>, F32RankK, 64>(s, a0, a1)
+                                    : launch_pair_tn_nt<F32Tile<64, 64, false, false>, F32RankK, 64>(s, a0, a1);
   if (dma_ok<false, false>(a0) && dma_ok<true, true>(a1))
     return launch_pair_tn_nt<F32DmaTile<false, false>, F32DmaTile<true, true>, 64>(s, a0, a1);
   return launch_pair_tn_nt<F32Tile<64, 64, false, false>, F32Tile<64, 64, true, true>, 64>(s, a0, a1);

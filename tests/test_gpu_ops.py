@@ -167,6 +167,32 @@ def test_skinny_products_with_epilogues(gpu, m, n, k):
     assert_near_exact(got, exact, cpu, floor=2e-5, what=f"NT+mask {m}x{n}x{k}")
     assert np.all(got[act <= 0] == 0)
 
+# NT products with K <= 16 (the dX of a narrow output layer) run on the
+# rank-K block: ragged M and N (edges of the 64x64 blocks, N not a multiple of
+# 4 for the scalar stores), K from 1 to 16, every epilogue.
+@pytest.mark.parametrize("m,n,k", [(1, 4, 1), (65, 130, 10), (100, 33, 7), (256, 1024, 16), (2048, 1024, 10)])
+def test_rank_k_nt_products_with_epilogues(gpu, m, n, k):
+    rng = np.random.default_rng(m + 3 * n + k)
+    d = rng.normal(size=(m, k)).astype(np.float32)
+    v = rng.normal(size=(n, k)).astype(np.float32)
+    gd, gv = gpu.upload(d), gpu.upload(v)
+    exact = d.astype(np.float64) @ v.astype(np.float64).T
+    cpu = O.matmul(d, v.T.copy())
+    out = gpu.zeros((m, n))
+    gpu.matmul_a_bt(gd, gv, out)
+    assert_near_exact(gpu.download(out), exact, cpu, floor=2e-5, what=f"NT {m}x{n}x{k}")
+    act = np.maximum(rng.normal(size=(m, n)).astype(np.float32), 0)
+    gpu.matmul_a_bt(gd, gv, out, relu_mask_from=gpu.upload(act))
+    got = gpu.download(out)
+    assert_near_exact(got, exact * (act > 0), cpu * (act > 0), floor=2e-5, what=f"NT+mask {m}x{n}x{k}")
+    assert np.all(got[act <= 0] == 0)
+    # integer operands: every order of the K products gives the exact sum
+    di = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    vi = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
+    gpu.matmul_a_bt(gpu.upload(di), gpu.upload(vi), out)
+    assert np.array_equal(gpu.download(out), (di.astype(np.float64) @ vi.T).astype(np.float32))
+
+
 @pytest.mark.parametrize("k,m,n", [(2048, 1024, 10), (64, 130, 96), (513, 64, 1024), (256, 128, 192)])
 def test_tn_gemm_fused_colsum(gpu, k, m, n):
     rng = np.random.default_rng(3)
