@@ -35,6 +35,7 @@
 // deterministic, no float atomics.
 
 #include "device_util.h"
+#include "optim_dev.h"
 #include "rt_internal.h"
 
 namespace {
@@ -702,6 +703,24 @@ __global__ __launch_bounds__(T0::THREADS) void gemm_f32_pair_kernel(F32Args p0, 
   }
 }
 
+// A GEMM and an optimizer update that does not touch its operands in one
+// launch: blocks [0, n_gemm) run the GEMM's (tile, K slice) items, the rest
+// the optimizer blocks of b.  The GEMM is dispatched first; the update, which
+// is HBM-bound, runs on the CUs next to its MFMA-bound tiles.
+template <class T>
+__global__ __launch_bounds__(T::THREADS) void gemm_f32_opt_kernel(F32Args p, rt_opt::OptBatch b, int n_gemm) {
+  static_assert(T::THREADS == rt_opt::kThreads, "one block size");
+  __shared__ __attribute__((aligned(16))) float smem[T::SMEM];
+  const int blk = blockIdx.x;
+  if (blk < n_gemm) {
+    const int tiles = p.tiles_m * p.tiles_n;
+    const int loc = xcd_local(blk, n_gemm);
+    T::run(p, loc % tiles, loc / tiles, smem);
+  } else {
+    rt_opt::optimizer_block<false>(b, blk - n_gemm);
+  }
+}
+
 // The first cs_blocks blocks each take 256 columns of the column sums: they
 // start first, so their chains of loads run under the plane sums; the rest
 // sum the planes (grid-stride over M*N).
@@ -1058,6 +1077,40 @@ hipError_t gemm_f32_launch(hipStream_t s, const GemmDesc& d) {
     case RT_NT: return dispatch_tile<true, true>(s, a);
   }
   return hipErrorInvalidValue;
+}
+
+template <class T, int BM, int BN>
+hipError_t launch_gemm_opt(hipStream_t s, F32Args a, const rt_opt::OptBatch& b, long long opt_blocks) {
+  a.tiles_m = (a.M + BM - 1) / BM;
+  a.tiles_n = (a.N + BN - 1) / BN;
+  const long long n_gemm = (long long)a.tiles_m * a.tiles_n * a.splits;
+  if (n_gemm + opt_blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  rt::launch((gemm_f32_opt_kernel<T>), dim3((unsigned)(n_gemm + opt_blocks)), dim3(T::THREADS), 0, s, a, b,
+             (int)n_gemm);
+  return hipGetLastError();
+}
+
+bool gemm_opt_supported(const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& P) {
+  if (d.in_dtype != RT_F32 || d.layout != RT_TN || d.M <= 0 || d.N <= 0 || d.K <= 0) return false;
+  return nt > 0 && optimizer_fits_cache(ts, nt, P);
+}
+
+hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& P) {
+  if (!gemm_opt_supported(d, ts, nt, P)) return hipErrorInvalidValue;
+  rt_opt::OptBatch b{};
+  long long opt_blocks = 0;
+  double bytes = 0.0;
+  hipError_t e = rt_opt::make_batch(ts, nt, P, b, &opt_blocks, &bytes);
+  if (e != hipSuccess) return e;
+  // The tile the TN GEMM's own launch would take (same bits).
+  const F32Args a = make_args(d);
+  switch (pick_tile(a)) {
+    case kT128: return launch_gemm_opt<F32Tile<128, 128, false, false>, 128, 128>(s, a, b, opt_blocks);
+    case kT64x32: return launch_gemm_opt<F32Tile<64, 32, false, false>, 64, 32>(s, a, b, opt_blocks);
+    default:
+      if (dma_ok<false, false>(a)) return launch_gemm_opt<F32DmaTile<false, false>, 64, 64>(s, a, b, opt_blocks);
+      return launch_gemm_opt<F32Tile<64, 64, false, false>, 64, 64>(s, a, b, opt_blocks);
+  }
 }
 
 bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1) {

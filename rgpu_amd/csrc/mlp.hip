@@ -244,18 +244,20 @@ static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float s
   return RT_OK;
 }
 
-// The optimizer's tensor list over the flat vectors: plain runs of segments
-// as one tensor each, and the W / b segments of layers whose dW planes are
-// still split as tensors that sum their planes first.
-static std::vector<OptTensor> opt_tensors(const rt_mlp* p) {
+// The optimizer's tensor list over the flat vectors of layers [l0, l1):
+// plain runs of segments as one tensor each, and the W / b segments of
+// layers whose dW planes are still split as tensors that sum their planes
+// first.
+static std::vector<OptTensor> opt_tensors(const rt_mlp* p, int l0, int l1) {
   std::vector<OptTensor> ts;
   auto seg = [&](size_t off, size_t n) {
     OptTensor T{p->theta + off, p->grad + off, p->m + off, p->v + off,
                 p->theta_h ? (void*)((unsigned short*)p->theta_h + off) : nullptr, n};
     return T;
   };
-  size_t run0 = 0;
-  for (int l = 0; l < p->n_layers; ++l) {
+  size_t run0 = p->L[l0].w_off;
+  const size_t end = l1 < p->n_layers ? p->L[l1].w_off : p->n_params;
+  for (int l = l0; l < l1; ++l) {
     const Layer& Ly = p->L[l];
     if (Ly.dw_parts == nullptr) continue;
     if (Ly.w_off > run0) ts.push_back(seg(run0, Ly.w_off - run0));
@@ -274,12 +276,45 @@ static std::vector<OptTensor> opt_tensors(const rt_mlp* p) {
     ts.push_back(Tb);
     run0 = Ly.b_off + Ly.dout;  // the b segment's padding stays untouched (zero)
   }
-  if (run0 < p->n_params) ts.push_back(seg(run0, p->n_params - run0));
+  if (run0 < end) ts.push_back(seg(run0, end - run0));
   return ts;
 }
 
+// The update's method and hyper-parameters (the step's t and flags are set
+// by the step itself).
+static OptParams plan_params(const rt_mlp* p) {
+  OptParams P;
+  P.kind = p->cfg.optimizer == RT_OPT_ADAM ? 0 : 1;
+  P.lr = p->cfg.lr;
+  P.beta1 = p->cfg.beta1;
+  P.beta2 = p->cfg.beta2;
+  P.eps = p->cfg.eps;
+  P.momentum = p->cfg.momentum;
+  return P;
+}
+
+static std::vector<OptTensor> plan_tensors(const rt_mlp* p, int l0, int l1, const OptParams& P) {
+  std::vector<OptTensor> ts = opt_tensors(p, l0, l1);
+  if (P.kind == 1 && P.momentum == 0.0f)
+    for (auto& T : ts) T.m = nullptr;
+  return ts;
+}
+
+// f32 plans: the update of layers 1.. (its gradients are final once layer
+// 1's backward has run) goes into layer 0's dW launch, its HBM-bound blocks
+// next to the GEMM's tiles; layer 0's own update follows.  Not under mixed
+// precision, whose update waits for the non-finite check of every gradient.
+static bool fuse_update(const rt_mlp* p) {
+  if (p->mixed || p->n_layers < 2) return false;
+  const OptParams P = plan_params(p);
+  const std::vector<OptTensor> ts = plan_tensors(p, 1, p->n_layers, P);
+  return optimizer_fits_cache(ts.data(), (int)ts.size(), P);
+}
+
+// Optimizer launches after the backward: layer 0's update alone when the
+// rest is fused into its dW launch, else the whole model's.
 static int opt_launches(const rt_mlp* p) {
-  const int n = (int)opt_tensors(p).size();
+  const int n = (int)opt_tensors(p, 0, fuse_update(p) ? 1 : p->n_layers).size();
   return (n + kMaxOptTensors - 1) / kMaxOptTensors;
 }
 
@@ -603,6 +638,29 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   }
   if ((rc = run_forward(p, x, labels, scale))) return rc;
 
+  // This step's update (t + 1), set up before the backward so that layer 0's
+  // dW launch can carry the update of layers 1.. (fuse_update).
+  OptParams P = plan_params(p);
+  if (P.kind == 0) {
+    const float c1 = 1.0f - powi_f32(P.beta1, p->t + 1), c2 = 1.0f - powi_f32(P.beta2, p->t + 1);
+    P.inv_c1 = 1.0f / c1;
+    P.inv_c2 = 1.0f / c2;
+  }
+  if (p->mixed) {
+    // Unscale exactly (the loss scale is a power of two in practice) and skip
+    // the whole update on a non-finite gradient; a skipped step does not
+    // advance Adam's t (the count lives on the device).
+    P.grad_scale = 1.0f / p->cfg.loss_scale;
+    P.skip_flag = overflow;
+    P.device_t = p->state;
+  }
+  // A label >= the classes skips the update (weights and moments stay as
+  // they were); an f32 plan counts the skipped step (in its first update
+  // launch) so that the report can take it back out of t.
+  P.skip_flag2 = p->state + 3;
+  const bool fuse = fuse_update(p);
+  bool fused = false;  // layers 1..'s update ran in layer 0's dW launch
+
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
   std::vector<char> unchecked(nl, 1);
   std::vector<ShareJob> jobs;
@@ -627,7 +685,15 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       if (rows > 0) jobs.push_back(ShareJob{Ly.cs_shares, p->grad + Ly.b_off, rows, (int)Ly.dout});
     }
     if (l == 0) {
-      {
+      const std::vector<OptTensor> rest = fuse ? plan_tensors(p, 1, nl, P) : std::vector<OptTensor>();
+      if (fuse && gemm_opt_supported(dw, rest.data(), (int)rest.size(), P)) {
+        OptParams Pr = P;
+        Pr.skip_count = p->state + 4;
+        Launch Lz(c, Ly.lbl_dw.c_str());
+        hipError_t e = gemm_opt_launch(c->stream, dw, rest.data(), (int)rest.size(), Pr);
+        if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
+        fused = true;
+      } else {
         Launch Lz(c, Ly.lbl_dw.c_str());
         hipError_t e = gemm_launch(c->stream, dw);
         if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
@@ -694,36 +760,10 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   }
 
   p->t += 1;
-  std::vector<OptTensor> ts = opt_tensors(p);
-  OptParams P;
-  P.kind = p->cfg.optimizer == RT_OPT_ADAM ? 0 : 1;
-  P.lr = p->cfg.lr;
-  P.beta1 = p->cfg.beta1;
-  P.beta2 = p->cfg.beta2;
-  P.eps = p->cfg.eps;
-  P.momentum = p->cfg.momentum;
-  if (P.kind == 0) {
-    const float c1 = 1.0f - powi_f32(P.beta1, p->t), c2 = 1.0f - powi_f32(P.beta2, p->t);
-    P.inv_c1 = 1.0f / c1;
-    P.inv_c2 = 1.0f / c2;
-  }
-  if (p->mixed) {
-    // Unscale exactly (the loss scale is a power of two in practice) and skip
-    // the whole update on a non-finite gradient; a skipped step does not
-    // advance Adam's t (the count lives on the device).
-    P.grad_scale = 1.0f / p->cfg.loss_scale;
-    P.skip_flag = overflow;
-    P.device_t = p->state;
-  }
-  // A label >= the classes skips the update (weights and moments stay as
-  // they were); an f32 plan counts the skipped step so that the report can
-  // take it back out of t.
-  P.skip_flag2 = p->state + 3;
-  if (P.kind == 1 && P.momentum == 0.0f)
-    for (auto& T : ts) T.m = nullptr;
+  const std::vector<OptTensor> ts = plan_tensors(p, 0, fused ? 1 : nl, P);
   for (size_t i0 = 0; i0 < ts.size(); i0 += kMaxOptTensors) {
     const int nt = (int)std::min<size_t>(kMaxOptTensors, ts.size() - i0);
-    P.skip_count = (!p->mixed && i0 == 0) ? p->state + 4 : nullptr;
+    P.skip_count = (!p->mixed && !fused && i0 == 0) ? p->state + 4 : nullptr;
     Launch Lz(c, "optimizer");
     hipError_t e = optimizer_launch(c->stream, ts.data() + i0, nt, P);
     if (e != hipSuccess) return hip_fail(c, e, "optimizer");

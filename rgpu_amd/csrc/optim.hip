@@ -19,158 +19,24 @@
 
 #include <algorithm>
 
+#include "optim_dev.h"
 #include "rt_internal.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kPerThread = 4;
-constexpr int kPerBlock = kThreads * kPerThread;
+using rt_opt::kPerBlock;
+using rt_opt::kThreads;
+using rt_opt::OptBatch;
 // MI355X's last-level (Infinity) cache: 256 MB.
 constexpr double kLastLevelCacheBytes = 256.0 * 1024 * 1024;
 
-struct OptBatch {
-  rt::OptTensor t[rt::kMaxOptTensors];
-  int block_start[rt::kMaxOptTensors + 1];
-  int nt;
-  rt::OptParams p;
-};
-
-__device__ inline unsigned short f32_to_bf16_rne(float x) {
-  unsigned int u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (unsigned short)(u >> 16);
-}
-
-__device__ inline float powi_dev(float a, int b) {
-  float r = 1.0f;
-  for (;;) {
-    if (b & 1) r *= a;
-    b /= 2;
-    if (b == 0) break;
-    a *= a;
-  }
-  return r;
-}
-
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef unsigned u2 __attribute__((ext_vector_type(2)));
-
-struct Coef {
-  float inv_c1, inv_c2;
-};
-
-// One element's update, the CPU expression order (optim.rs:88-95, 187-195).
-// m / v are read only where the method uses them.
-__device__ inline void update(const rt::OptParams& P, Coef c, float graw, float& th, float* m, float* v) {
-  const float g = graw * P.grad_scale;
-  if (P.kind == 0) {
-    const float mi = *m * P.beta1 + g * (1.0f - P.beta1);
-    const float vi = *v * P.beta2 + (g * g) * (1.0f - P.beta2);
-    *m = mi;
-    *v = vi;
-    const float m_hat = mi * c.inv_c1;
-    const float v_hat = vi * c.inv_c2;
-    th = th - (m_hat / (sqrtf(v_hat) + P.eps)) * P.lr;
-  } else if (P.momentum == 0.0f) {
-    th = th - g * P.lr;
-  } else {
-    const float vel = *m * P.momentum + g * P.lr;
-    *m = vel;
-    th = th - vel;
-  }
-}
-
-// Each thread owns 4 consecutive elements: one float4 of every stream when
-// the tensor allows it (T.vec), else four scalars.  STREAM: the launch moves
-// more than the last-level cache holds, so its float4 streams are read and
-// written non-temporally (measured: the 138 M-parameter Adam launch ~50 us
-// faster; a launch that fits is slower that way, its state no longer cached
-// for the next step).
+// STREAM: the launch moves more than the last-level cache holds, so its
+// float4 streams are read and written non-temporally (measured: the 138
+// M-parameter Adam launch ~50 us faster; a launch that fits is slower that
+// way, its state no longer cached for the next step).
 template <bool STREAM>
 __global__ __launch_bounds__(kThreads) void optimizer_kernel(OptBatch b) {
-  if ((b.p.skip_flag != nullptr && *b.p.skip_flag != 0) || (b.p.skip_flag2 != nullptr && *b.p.skip_flag2 != 0)) {
-    if (b.p.skip_count != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *b.p.skip_count += 1;
-    return;
-  }
-  Coef c{b.p.inv_c1, b.p.inv_c2};
-  if (b.p.device_t != nullptr) {
-    const int t = *b.p.device_t + 1;
-    c.inv_c1 = 1.0f / (1.0f - powi_dev(b.p.beta1, t));
-    c.inv_c2 = 1.0f / (1.0f - powi_dev(b.p.beta2, t));
-  }
-  const int blk = blockIdx.x;
-  int ti = 0;
-  while (ti + 1 < b.nt && b.block_start[ti + 1] <= blk) ++ti;
-  const rt::OptTensor& T = b.t[ti];
-  const rt::OptParams& P = b.p;
-  const long long i0 = (long long)(blk - b.block_start[ti]) * kPerBlock + (long long)kPerThread * threadIdx.x;
-  if (i0 >= (long long)T.n) return;
-  const bool adam = P.kind == 0, has_m = T.m != nullptr;
-
-  if (T.vec && i0 + 4 <= (long long)T.n) {
-    auto ld = [](const float* q) {
-      if constexpr (STREAM) return __builtin_nontemporal_load(reinterpret_cast<const f4*>(q));
-      else return *reinterpret_cast<const f4*>(q);
-    };
-    auto st = [](float* q, f4 x) {
-      if constexpr (STREAM) __builtin_nontemporal_store(x, reinterpret_cast<f4*>(q));
-      else *reinterpret_cast<f4*>(q) = x;
-    };
-    f4 g;
-    if (T.parts != nullptr) {
-      g = ld(T.parts + i0);
-#pragma unroll 4
-      for (int s = 1; s < T.n_parts; ++s) g = g + ld(T.parts + (long long)s * T.part_stride + i0);
-      st(T.grad_store + i0, g);
-    } else {
-      g = ld(T.grad + i0);
-    }
-    f4 th = ld(T.theta + i0);
-    f4 m = has_m ? ld(T.m + i0) : f4{0, 0, 0, 0};
-    f4 v = adam ? ld(T.v + i0) : f4{0, 0, 0, 0};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float te = th[e], me = m[e], ve = v[e];
-      update(P, c, g[e], te, &me, &ve);
-      th[e] = te;
-      m[e] = me;
-      v[e] = ve;
-    }
-    st(T.theta + i0, th);
-    if (has_m) st(T.m + i0, m);
-    if (adam) st(T.v + i0, v);
-    if (T.half_copy != nullptr) {  // 8-byte aligned (T.vec)
-      u2 w;
-      w[0] = (unsigned)f32_to_bf16_rne(th[0]) | ((unsigned)f32_to_bf16_rne(th[1]) << 16);
-      w[1] = (unsigned)f32_to_bf16_rne(th[2]) | ((unsigned)f32_to_bf16_rne(th[3]) << 16);
-      u2* h = reinterpret_cast<u2*>(static_cast<unsigned short*>(T.half_copy) + i0);
-      if constexpr (STREAM) __builtin_nontemporal_store(w, h);
-      else *h = w;
-    }
-    return;
-  }
-#pragma unroll
-  for (int e = 0; e < kPerThread; ++e) {
-    const long long i = i0 + e;
-    if (i >= (long long)T.n) break;
-    float graw;
-    if (T.parts != nullptr) {
-      graw = T.parts[i];
-      for (int s = 1; s < T.n_parts; ++s) graw = graw + T.parts[(long long)s * T.part_stride + i];
-      T.grad_store[i] = graw;
-    } else {
-      graw = T.grad[i];
-    }
-    float th = T.theta[i];
-    float mi = has_m ? T.m[i] : 0.0f, vi = adam ? T.v[i] : 0.0f;
-    update(P, c, graw, th, &mi, &vi);
-    if (has_m) T.m[i] = mi;
-    if (adam) T.v[i] = vi;
-    T.theta[i] = th;
-    if (T.half_copy != nullptr) static_cast<unsigned short*>(T.half_copy)[i] = f32_to_bf16_rne(th);
-  }
+  rt_opt::optimizer_block<STREAM>(b, blockIdx.x);
 }
 
 struct NonFiniteArgs {
@@ -230,6 +96,38 @@ __global__ void step_begin_kernel(int* state) {
 
 }  // namespace
 
+namespace rt_opt {
+
+hipError_t make_batch(const rt::OptTensor* ts, int nt, const rt::OptParams& p, OptBatch& b, long long* blocks,
+                      double* bytes) {
+  if (nt < 0 || nt > rt::kMaxOptTensors) return hipErrorInvalidValue;
+  b.nt = nt;
+  b.p = p;
+  long long nb = 0;
+  double by = 0.0;
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  for (int i = 0; i < nt; ++i) {
+    b.t[i] = ts[i];
+    const rt::OptTensor& T = ts[i];
+    // float4 streams: every base 16-byte aligned (the bf16 copy 8-byte) and
+    // the partial planes 4-float strided.
+    b.t[i].vec = al16(T.theta) && al16(T.grad) && (T.m == nullptr || al16(T.m)) && (T.v == nullptr || al16(T.v)) &&
+                 (T.half_copy == nullptr || (reinterpret_cast<uintptr_t>(T.half_copy) & 7) == 0) &&
+                 (T.parts == nullptr || (al16(T.parts) && al16(T.grad_store) && T.part_stride % 4 == 0));
+    b.block_start[i] = (int)nb;
+    nb += (long long)((ts[i].n + kPerBlock - 1) / kPerBlock);
+    const int streams = 2 + (T.m ? 2 : 0) + (p.kind == 0 ? 2 : 0) + (T.parts ? T.n_parts + 1 : 1);
+    by += (double)T.n * (4.0 * streams + (T.half_copy ? 2.0 : 0.0));
+  }
+  b.block_start[nt] = (int)nb;
+  if (nb > 0x7fffffffLL) return hipErrorInvalidValue;
+  *blocks = nb;
+  *bytes = by;
+  return hipSuccess;
+}
+
+}  // namespace rt_opt
+
 namespace rt {
 
 hipError_t step_begin_launch(hipStream_t s, int* state) {
@@ -253,34 +151,24 @@ float powi_f32(float a, int b) {
 
 hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const OptParams& p) {
   if (nt <= 0) return hipSuccess;
-  if (nt > kMaxOptTensors) return hipErrorInvalidValue;
   OptBatch b{};
-  b.nt = nt;
-  b.p = p;
   long long blocks = 0;
-  double bytes = 0.0;  // HBM bytes the launch moves
-  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-  for (int i = 0; i < nt; ++i) {
-    b.t[i] = ts[i];
-    const OptTensor& T = ts[i];
-    // float4 streams: every base 16-byte aligned (the bf16 copy 8-byte) and
-    // the partial planes 4-float strided.
-    b.t[i].vec = al16(T.theta) && al16(T.grad) && (T.m == nullptr || al16(T.m)) && (T.v == nullptr || al16(T.v)) &&
-                 (T.half_copy == nullptr || (reinterpret_cast<uintptr_t>(T.half_copy) & 7) == 0) &&
-                 (T.parts == nullptr || (al16(T.parts) && al16(T.grad_store) && T.part_stride % 4 == 0));
-    b.block_start[i] = (int)blocks;
-    blocks += (long long)((ts[i].n + kPerBlock - 1) / kPerBlock);
-    const int streams = 2 + (T.m ? 2 : 0) + (p.kind == 0 ? 2 : 0) + (T.parts ? T.n_parts + 1 : 1);
-    bytes += (double)T.n * (4.0 * streams + (T.half_copy ? 2.0 : 0.0));
-  }
-  b.block_start[nt] = (int)blocks;
-  if (blocks == 0) return hipSuccess;
-  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  double bytes = 0.0;
+  hipError_t e = rt_opt::make_batch(ts, nt, p, b, &blocks, &bytes);
+  if (e != hipSuccess || blocks == 0) return e;
   if (bytes > kLastLevelCacheBytes)
     rt::launch(optimizer_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, b);
   else
     rt::launch(optimizer_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, b);
   return hipGetLastError();
+}
+
+bool optimizer_fits_cache(const OptTensor* ts, int nt, const OptParams& p) {
+  OptBatch b{};
+  long long blocks = 0;
+  double bytes = 0.0;
+  return nt <= kMaxOptTensors && rt_opt::make_batch(ts, nt, p, b, &blocks, &bytes) == hipSuccess &&
+         bytes <= kLastLevelCacheBytes;
 }
 
 hipError_t nonfinite_check_launch(hipStream_t s, const float* const* ptrs, const size_t* ns, int nt, int* flag,

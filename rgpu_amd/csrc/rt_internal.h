@@ -274,6 +274,14 @@ struct OptParams {
 hipError_t step_begin_launch(hipStream_t s, int* state);
 constexpr int kMaxOptTensors = 24;
 hipError_t optimizer_launch(hipStream_t s, const OptTensor* ts, int nt, const OptParams& p);
+// The update of ts fits one launch and moves no more than the last-level
+// cache holds (so it takes the cached, not the streaming, path).
+bool optimizer_fits_cache(const OptTensor* ts, int nt, const OptParams& p);
+// An f32 TN GEMM (a weight gradient) and an optimizer update of other
+// tensors in one launch: the GEMM gives the bits of its own launch, the
+// update those of optimizer_launch.  For updates that fit the cache.
+bool gemm_opt_supported(const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& p);
+hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& p);
 // Column sums of a whole (unsplit) half GEMM left as shares: dst[j] = the
 // rows src[t * n + j], t = 0 .. rows-1, added in order from zero (what the
 // GEMM's own shares launch computes).
