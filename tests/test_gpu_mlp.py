@@ -155,6 +155,28 @@ def test_config_batch32_sgd_one_step(gpu):
               [w - p for w, p in zip(mlp.weights(), p0)], 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("dims,batch,opt,lr", [([512, 1024, 1024, 10], 2048, "adam", 1e-3),
+                                              ([512, 1024, 1024, 10], 32, "sgd", 0.01),
+                                              ([64, 128, 96, 48, 10], 256, "adam", 1e-2)])
+def test_plan_update_is_the_optimizer_entry_point_on_its_gradients(gpu, dims, batch, opt, lr):
+    # An f32 plan runs the update of layers 1.. inside layer 0's dW launch and
+    # layer 0's after it: after one step every weight is, bit for bit,
+    # rt_adam / rt_sgd applied to its initial value and the plan's gradient.
+    params = kaiming_model(5, dims)
+    x = normal_batch(105, batch, dims[0])
+    lab = uniform_labels(106, batch, dims[-1])
+    kw = {"optimizer": "sgd"} if opt == "sgd" else {}
+    mlp = G.GpuMlp.from_params(gpu, params, batch, lr, **kw)
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+    for p0, g, w in zip(params, mlp.grads(), mlp.weights()):
+        th = gpu.upload(p0.reshape(w.shape))
+        if opt == "adam":
+            gpu.adam(th, gpu.zeros(w.shape), gpu.zeros(w.shape), gpu.upload(g), lr, (0.9, 0.999), 1)
+        else:
+            gpu.sgd(th, gpu.upload(g), lr)
+        assert np.array_equal(gpu.download(th).view(np.uint32), w.view(np.uint32)), w.shape
+
+
 def test_config_batch2048_adam_100_steps(gpu):
     # MLP 512->1024->1024->10 f32 at batch 2048, Adam(1e-3, 0.9, 0.999, 1e-8),
     # 100 steps on fresh seeded N(0,1) batches; per-step loss and final weights.
