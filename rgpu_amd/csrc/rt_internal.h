@@ -183,6 +183,10 @@ struct GemmDesc {
   int* nf_flag = nullptr;
 };
 bool gemm_checks_nonfinite(const GemmDesc& d);
+// Narrow f32 NN products (<= 16 columns) go to the output-layer kernel, in
+// rt_gemm and in a one-slice split-K alike.
+bool narrow_nn(const GemmDesc& d);
+hipError_t narrow_nn_launch(hipStream_t s, const GemmDesc& d);
 size_t colsum_scratch_need(int M, int N, int splits);
 // Rows of column-sum shares per K slice that a cs_shares_to_caller launch of
 // d leaves in cs_scratch (0: it writes colsum_partials itself).

@@ -471,17 +471,9 @@ int rt_gemm(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_bu
     d.mask_dtype = aux->dtype;
   }
   d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
-  // A narrow f32 NN product (an output layer's logits, <= 16 columns) has
-  // too few output tiles for the tiled kernels to be anything but latency
-  // bound; the output-layer kernel splits its K over 8 waves of a block per
-  // 16 rows instead.
-  if (layout == RT_NN && a->dtype == RT_F32 && (epi == RT_EPI_NONE || epi == RT_EPI_BIAS) &&
-      head_xent_supported(d.K, d.N) && d.lda == d.K && (reinterpret_cast<uintptr_t>(d.A) & 15) == 0) {
+  if (narrow_nn(d)) {
     Launch L(c, "gemm_nn");
-    HIP_TRY(c,
-            head_xent_launch(c->stream, static_cast<const float*>(d.A), d.K, static_cast<const float*>(d.B), d.bias,
-                             nullptr, static_cast<float*>(d.C), nullptr, nullptr, d.M, d.N, 0.0f, nullptr),
-            "gemm launch");
+    HIP_TRY(c, narrow_nn_launch(c->stream, d), "gemm launch");
     return RT_OK;
   }
   if (colsum && is_half(a->dtype)) {
@@ -573,6 +565,22 @@ int splitk_check(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, 
   return RT_OK;
 }
 
+// A narrow f32 NN product (an output layer's logits, <= 16 columns) has too
+// few output tiles for the tiled kernels to be anything but latency bound;
+// the output-layer kernel splits its K over 8 waves of a block per 16 rows
+// instead.  rt_gemm and a one-slice split-K both route it there, so that a
+// split-K of one slice gives the whole GEMM's bits.
+bool narrow_nn(const GemmDesc& d) {
+  return d.layout == RT_NN && d.in_dtype == RT_F32 && (d.epi == RT_EPI_NONE || d.epi == RT_EPI_BIAS) &&
+         d.colsum == nullptr && d.splits <= 1 && head_xent_supported(d.K, d.N) && d.lda == d.K &&
+         (reinterpret_cast<uintptr_t>(d.A) & 15) == 0;
+}
+
+hipError_t narrow_nn_launch(hipStream_t s, const GemmDesc& d) {
+  return head_xent_launch(s, static_cast<const float*>(d.A), d.K, static_cast<const float*>(d.B), d.bias, nullptr,
+                          static_cast<float*>(d.C), nullptr, nullptr, d.M, d.N, 0.0f, nullptr);
+}
+
 int splitk_run(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt_buf* out, size_t slices,
                rt_buf* colsum, size_t M, size_t N, size_t K, float* part, float* cs_scratch, size_t cs_elems) {
   GemmDesc d;
@@ -595,7 +603,7 @@ int splitk_run(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_buf* b, rt
     d.C = out->ptr;
     d.colsum = colsum ? static_cast<float*>(colsum->ptr) : nullptr;
     Launch L(c, "splitk_gemm");
-    HIP_TRY(c, gemm_launch(c->stream, d), "split-K gemm");
+    HIP_TRY(c, narrow_nn(d) ? narrow_nn_launch(c->stream, d) : gemm_launch(c->stream, d), "split-K gemm");
     return RT_OK;
   }
   d.C = part;

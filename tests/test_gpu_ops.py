@@ -209,7 +209,9 @@ def test_tn_gemm_fused_colsum(gpu, k, m, n):
     assert np.array_equal(gpu.download(cs).reshape(-1), di.sum(0, dtype=np.float64).astype(np.float32))
 
 
-@pytest.mark.parametrize("m,n,k", [(64, 64, 4096), (32, 96, 2048), (128, 64, 1024)])
+# N = 10 and 7: the reduction's scalar path (rows not a multiple of four
+# floats); slices 1..16 take the eight-plane loop and the tail.
+@pytest.mark.parametrize("m,n,k", [(64, 64, 4096), (32, 96, 2048), (128, 64, 1024), (50, 10, 2048), (33, 7, 1024)])
 def test_split_k_against_whole_gemm(gpu, m, n, k):  # gpu.rs:383-430
     a, b = sincos(m, k, n)
     want = O.matmul(a, b)
