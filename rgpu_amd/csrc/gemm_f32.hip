@@ -389,6 +389,11 @@ __device__ void F32Tile<BM, BN, A_KC, B_KC, BK, KS, PF>::run(const F32Args& p, i
 //     four k of the lane's four MFMA steps);
 //   M/N-contiguous [k][64]: 64-byte chunk c of row k at c ^ ((k >> 2) & 3); a
 //     fragment is four b32 reads (k = 16 half + 4g + s, column 16u + r).
+// A tile's plain stores (F32Dma::run's default epilogue).
+struct NoEpi {
+  static constexpr bool kOn = false;
+};
+
 struct F32Dma {
   static constexpr int BM = 64, BN = 64, BK = 32, THREADS = 256, WAVES = 4;
   static constexpr int TM = 2, TN = 2;                 // 16x16 MFMA tiles per wave (32x32 wave tile)
@@ -444,8 +449,8 @@ struct F32Dma {
     }
   };
 
-  template <bool A_KC, bool B_KC>
-  __device__ static void run(const F32Args& p, int bid, int split, float* smem);
+  template <bool A_KC, bool B_KC, class Epi = NoEpi>
+  __device__ static void run(const F32Args& p, int bid, int split, float* smem, const Epi& e = Epi{});
 };
 
 template <int EPI>
@@ -477,8 +482,8 @@ __device__ __forceinline__ void f32_store_direct(const F32Args& p, const f4 (&ac
   }
 }
 
-template <bool A_KC, bool B_KC>
-__device__ void F32Dma::run(const F32Args& p, int bid, int split, float* smem) {
+template <bool A_KC, bool B_KC, class Epi>
+__device__ void F32Dma::run(const F32Args& p, int bid, int split, float* smem, const Epi& e) {
   using OpA = Op<A_KC>;
   using OpB = Op<B_KC>;
   auto sA = [&](int buf) { return smem + buf * STAGE; };
@@ -586,10 +591,14 @@ __device__ void F32Dma::run(const F32Args& p, int bid, int split, float* smem) {
     __syncthreads();
     if (tid < 64) {
       const float v = ((red[tid] + red[64 + tid]) + red[128 + tid]) + red[192 + tid];
-      p.colsum[(long long)split * p.N + n0 + tid] = v;
+      if constexpr (Epi::kOn)
+        e.bias(p, n0 + tid, v);
+      else
+        p.colsum[(long long)split * p.N + n0 + tid] = v;
     }
   }
 
+  if constexpr (Epi::kOn) return e.tile(p, acc, m0, n0, wm, wn, g, r);
   if (p.splits > 1) return f32_store_direct<RT_EPI_NONE>(p, acc, m0, n0, wm, wn, g, r, split);
   switch (p.epi) {
     case RT_EPI_BIAS: return f32_store_direct<RT_EPI_BIAS>(p, acc, m0, n0, wm, wn, g, r, split);
@@ -716,6 +725,73 @@ __global__ __launch_bounds__(T::THREADS) void gemm_f32_opt_kernel(F32Args p, rt_
     const int tiles = p.tiles_m * p.tiles_n;
     const int loc = xcd_local(blk, n_gemm);
     T::run(p, loc % tiles, loc / tiles, smem);
+  } else {
+    rt_opt::optimizer_block<false>(b, blk - n_gemm);
+  }
+}
+
+// The update of the layer whose dW this unsplit TN launch computes, done by
+// the tiles themselves: an element's gradient is final in the tile that
+// computed it, so the tile stores it and updates the parameter and its
+// optimizer state there, with the optimizer's per-element arithmetic (same
+// bits as the separate update); the first row of tiles does the same for the
+// bias from its column sums.  w / b index like dW / db (w.n = M·N, ldc = N).
+struct UpdEpi {
+  static constexpr bool kOn = true;
+  rt::OptTensor w, b;
+  rt::OptParams P;
+  __device__ void tile(const F32Args& p, const f4 (&acc)[2][2], int m0, int n0, int wm, int wn, int g,
+                       int r) const {
+    const bool skip = rt_opt::skipped(P);
+    const rt_opt::Coef c = rt_opt::coef(P);
+    const bool adam = P.kind == 0, has_m = w.m != nullptr;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const long long row_off = (long long)(m0 + wm + 16 * t + r) * p.ldc;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const long long i = row_off + n0 + wn + 16 * u + 4 * g;
+        const f4 gv = acc[t][u];
+        *reinterpret_cast<f4*>(p.C + i) = gv;
+        if (skip) continue;
+        f4 th = *reinterpret_cast<const f4*>(w.theta + i);
+        f4 m = has_m ? *reinterpret_cast<const f4*>(w.m + i) : f4{0, 0, 0, 0};
+        f4 v = adam ? *reinterpret_cast<const f4*>(w.v + i) : f4{0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float te = th[q], me = m[q], ve = v[q];
+          rt_opt::update(P, c, gv[q], te, &me, &ve);
+          th[q] = te;
+          m[q] = me;
+          v[q] = ve;
+        }
+        *reinterpret_cast<f4*>(w.theta + i) = th;
+        if (has_m) *reinterpret_cast<f4*>(w.m + i) = m;
+        if (adam) *reinterpret_cast<f4*>(w.v + i) = v;
+      }
+    }
+  }
+  __device__ void bias(const F32Args& p, int col, float gv) const {
+    p.colsum[col] = gv;
+    if (rt_opt::skipped(P)) return;
+    const bool adam = P.kind == 0, has_m = b.m != nullptr;
+    float th = b.theta[col], m = has_m ? b.m[col] : 0.0f, v = adam ? b.v[col] : 0.0f;
+    rt_opt::update(P, rt_opt::coef(P), gv, th, &m, &v);
+    b.theta[col] = th;
+    if (has_m) b.m[col] = m;
+    if (adam) b.v[col] = v;
+  }
+};
+
+// gemm_f32_opt_kernel on 64x64 DMA tiles of an unsplit TN product whose
+// tiles also update their own layer (UpdEpi).
+__global__ __launch_bounds__(F32Dma::THREADS) void gemm_f32_opt_upd_kernel(F32Args p, rt_opt::OptBatch b, int n_gemm,
+                                                                          UpdEpi u) {
+  static_assert(F32Dma::THREADS == rt_opt::kThreads, "one block size");
+  __shared__ __attribute__((aligned(16))) float smem[F32Dma::SMEM];
+  const int blk = blockIdx.x;
+  if (blk < n_gemm) {
+    F32Dma::run<false, false>(p, xcd_local(blk, n_gemm), 0, smem, u);
   } else {
     rt_opt::optimizer_block<false>(b, blk - n_gemm);
   }
@@ -1095,15 +1171,46 @@ bool gemm_opt_supported(const GemmDesc& d, const OptTensor* ts, int nt, const Op
   return nt > 0 && optimizer_fits_cache(ts, nt, P);
 }
 
-hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& P) {
+bool gemm_opt_update_ok(const GemmDesc& d, const OptTensor* wb, const OptParams& P) {
+  if (d.in_dtype != RT_F32 || d.layout != RT_TN || d.splits > 1 || d.epi != RT_EPI_NONE || d.colsum == nullptr ||
+      d.ldc != d.N || d.M <= 0 || d.N <= 0 || d.K <= 0)
+    return false;
+  // The tile the TN GEMM's own launch would take: 64x64 DMA tiles.
+  const F32Args a = make_args(d);
+  if (pick_tile(a) != kT64 || !dma_ok<false, false>(a)) return false;
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+  const OptTensor &W = wb[0], &Bt = wb[1];
+  const bool adam = P.kind == 0, need_m = adam || P.momentum != 0.0f;
+  for (const OptTensor* T : {&W, &Bt}) {
+    if (T->theta == nullptr || T->parts != nullptr || T->half_copy != nullptr) return false;
+    if (need_m != (T->m != nullptr) || (adam && T->v == nullptr)) return false;
+  }
+  return W.n == (size_t)d.M * d.N && Bt.n == (size_t)d.N && W.grad == d.C && Bt.grad == d.colsum &&
+         al16(W.theta) && (W.m == nullptr || al16(W.m)) && (!adam || al16(W.v));
+}
+
+hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& P,
+                           const OptTensor* upd) {
   if (!gemm_opt_supported(d, ts, nt, P)) return hipErrorInvalidValue;
+  if (upd != nullptr && !gemm_opt_update_ok(d, upd, P)) return hipErrorInvalidValue;
   rt_opt::OptBatch b{};
   long long opt_blocks = 0;
   double bytes = 0.0;
   hipError_t e = rt_opt::make_batch(ts, nt, P, b, &opt_blocks, &bytes);
   if (e != hipSuccess) return e;
   // The tile the TN GEMM's own launch would take (same bits).
-  const F32Args a = make_args(d);
+  F32Args a = make_args(d);
+  if (upd != nullptr) {
+    a.tiles_m = a.M / 64;
+    a.tiles_n = a.N / 64;
+    const long long n_gemm = (long long)a.tiles_m * a.tiles_n;
+    if (n_gemm + opt_blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+    UpdEpi u{upd[0], upd[1], P};
+    u.P.skip_count = nullptr;  // counted by the optimizer blocks of the launch
+    rt::launch(gemm_f32_opt_upd_kernel, dim3((unsigned)(n_gemm + opt_blocks)), dim3(F32Dma::THREADS), 0, s, a, b,
+               (int)n_gemm, u);
+    return hipGetLastError();
+  }
   switch (pick_tile(a)) {
     case kT128: return launch_gemm_opt<F32Tile<128, 128, false, false>, 128, 128>(s, a, b, opt_blocks);
     case kT64x32: return launch_gemm_opt<F32Tile<64, 32, false, false>, 64, 32>(s, a, b, opt_blocks);

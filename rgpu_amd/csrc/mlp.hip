@@ -27,6 +27,7 @@
 // reduction, chosen by rt_splitk_slices.
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -311,9 +312,40 @@ static bool fuse_update(const rt_mlp* p) {
   return optimizer_fits_cache(ts.data(), (int)ts.size(), P);
 }
 
-// Optimizer launches after the backward: layer 0's update alone when the
-// rest is fused into its dW launch, else the whole model's.
-static int opt_launches(const rt_mlp* p) {
+// Layer 0's W and b as the targets of an update done by its own dW tiles.
+static std::array<OptTensor, 2> layer0_update(const rt_mlp* p, const OptParams& P) {
+  const Layer& L0 = p->L[0];
+  auto seg = [&](size_t off, size_t n) {
+    OptTensor T{p->theta + off, p->grad + off, p->m + off, p->v + off, nullptr, n};
+    if (P.kind == 1 && P.momentum == 0.0f) T.m = nullptr;
+    return T;
+  };
+  return {seg(L0.w_off, L0.din * L0.dout), seg(L0.b_off, L0.dout)};
+}
+
+// Layer 0's dW of an f32 plan as one unsplit launch of DMA tiles: with the
+// update of layers 1.. in the same launch (fuse_update), its tiles also
+// update layer 0 itself (gemm_opt_update_ok), and the step has no optimizer
+// launch of its own.
+static bool update_in_tiles(const rt_mlp* p, const GemmDesc& dw) {
+  if (!fuse_update(p) || p->L[0].dw_parts != nullptr || p->L[0].splits_dw > 1) return false;
+  const OptParams P = plan_params(p);
+  return gemm_opt_update_ok(dw, layer0_update(p, P).data(), P);
+}
+// Layer 0's f32 dW launch as the step builds it for the batch x (any 16-byte
+// aligned pointer, nullptr included, gives the step's tile decisions).
+static GemmDesc layer0_dw(rt_mlp* p, const void* x) {
+  const Layer& L0 = p->L[0];
+  return plan_desc(p, RT_TN, RT_F32, x, L0.delta, p->grad + L0.w_off, RT_F32, (int)L0.din, (int)L0.dout,
+                   (int)p->batch, (int)L0.din, (int)L0.ldh, RT_EPI_NONE, nullptr, nullptr, RT_F32,
+                   p->grad + L0.b_off, L0.splits_dw, L0.dw_parts);
+}
+
+// Optimizer launches after the backward: none when layer 0's dW tiles do
+// its update, layer 0's update alone when the rest is fused into its dW
+// launch, else the whole model's.
+static int opt_launches(rt_mlp* p) {
+  if (!p->mixed && update_in_tiles(p, layer0_dw(p, nullptr))) return 0;
   const int n = (int)opt_tensors(p, 0, fuse_update(p) ? 1 : p->n_layers).size();
   return (n + kMaxOptTensors - 1) / kMaxOptTensors;
 }
@@ -660,6 +692,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   P.skip_flag2 = p->state + 3;
   const bool fuse = fuse_update(p);
   bool fused = false;  // layers 1..'s update ran in layer 0's dW launch
+  bool upd0 = false;   // and layer 0's in that launch's tiles
 
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
   std::vector<char> unchecked(nl, 1);
@@ -689,8 +722,10 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       if (fuse && gemm_opt_supported(dw, rest.data(), (int)rest.size(), P)) {
         OptParams Pr = P;
         Pr.skip_count = p->state + 4;
+        upd0 = update_in_tiles(p, dw);
+        const std::array<OptTensor, 2> wb = layer0_update(p, P);
         Launch Lz(c, Ly.lbl_dw.c_str());
-        hipError_t e = gemm_opt_launch(c->stream, dw, rest.data(), (int)rest.size(), Pr);
+        hipError_t e = gemm_opt_launch(c->stream, dw, rest.data(), (int)rest.size(), Pr, upd0 ? wb.data() : nullptr);
         if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
         fused = true;
       } else {
@@ -760,6 +795,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   }
 
   p->t += 1;
+  if (upd0) return RT_OK;
   const std::vector<OptTensor> ts = plan_tensors(p, 0, fused ? 1 : nl, P);
   for (size_t i0 = 0; i0 < ts.size(); i0 += kMaxOptTensors) {
     const int nt = (int)std::min<size_t>(kMaxOptTensors, ts.size() - i0);

@@ -53,6 +53,25 @@ struct Coef {
   float inv_c1, inv_c2;
 };
 
+// Whether this step's update is skipped (a non-finite gradient or a label
+// past the classes).
+__device__ inline bool skipped(const rt::OptParams& P) {
+  return (P.skip_flag != nullptr && *P.skip_flag != 0) || (P.skip_flag2 != nullptr && *P.skip_flag2 != 0);
+}
+
+// Adam's bias corrections of this update: from the host, or from the device
+// step count (*device_t + 1 = this update's t).
+__device__ inline Coef coef(const rt::OptParams& P) {
+#pragma clang fp contract(off)
+  Coef c{P.inv_c1, P.inv_c2};
+  if (P.device_t != nullptr) {
+    const int t = *P.device_t + 1;
+    c.inv_c1 = 1.0f / (1.0f - powi_dev(P.beta1, t));
+    c.inv_c2 = 1.0f / (1.0f - powi_dev(P.beta2, t));
+  }
+  return c;
+}
+
 // One element's update, the CPU expression order (optim.rs:88-95, 187-195).
 // m / v are read only where the method uses them.
 __device__ inline void update(const rt::OptParams& P, Coef c, float graw, float& th, float* m, float* v) {
@@ -84,16 +103,11 @@ __device__ inline void update(const rt::OptParams& P, Coef c, float graw, float&
 template <bool STREAM>
 __device__ inline void optimizer_block(const OptBatch& b, int blk) {
 #pragma clang fp contract(off)
-  if ((b.p.skip_flag != nullptr && *b.p.skip_flag != 0) || (b.p.skip_flag2 != nullptr && *b.p.skip_flag2 != 0)) {
+  if (skipped(b.p)) {
     if (b.p.skip_count != nullptr && blk == 0 && threadIdx.x == 0) *b.p.skip_count += 1;
     return;
   }
-  Coef c{b.p.inv_c1, b.p.inv_c2};
-  if (b.p.device_t != nullptr) {
-    const int t = *b.p.device_t + 1;
-    c.inv_c1 = 1.0f / (1.0f - powi_dev(b.p.beta1, t));
-    c.inv_c2 = 1.0f / (1.0f - powi_dev(b.p.beta2, t));
-  }
+  const Coef c = coef(b.p);
   int ti = 0;
   while (ti + 1 < b.nt && b.block_start[ti + 1] <= blk) ++ti;
   const rt::OptTensor& T = b.t[ti];

@@ -284,8 +284,13 @@ bool optimizer_fits_cache(const OptTensor* ts, int nt, const OptParams& p);
 // An f32 TN GEMM (a weight gradient) and an optimizer update of other
 // tensors in one launch: the GEMM gives the bits of its own launch, the
 // update those of optimizer_launch.  For updates that fit the cache.
+// With upd = {W, b} (gemm_opt_update_ok) the GEMM's tiles also update W and
+// b from the dW (d.C) and db (d.colsum) they compute, as optimizer_launch
+// would on those gradients.
 bool gemm_opt_supported(const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& p);
-hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& p);
+bool gemm_opt_update_ok(const GemmDesc& d, const OptTensor* wb, const OptParams& p);
+hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& p,
+                           const OptTensor* upd = nullptr);
 // Column sums of a whole (unsplit) half GEMM left as shares: dst[j] = the
 // rows src[t * n + j], t = 0 .. rows-1, added in order from zero (what the
 // GEMM's own shares launch computes).

@@ -111,9 +111,11 @@ def test_small_batch_plan_follows_cpu(gpu, batch, dims, steps):
     loss, mlp = _trajectory(gpu, x, lab, dims, 3, steps, 1e-3)
     # Launches: the 2 hidden forwards (each + its reduction when split), the
     # fused head and loss, the head's dW+dX pair, layer 1's dW and dX (+ its
-    # reduction when split), layer 0's dW, the optimizer.
+    # reduction when split), layer 0's dW, whose launch also updates layers
+    # 1.. and whose tiles update layer 0 (its K of at most 96 is not split):
+    # no optimizer launch.
     red = 0 if skinny[0] else 1
-    assert mlp.dispatches_por_passo() == 2 * (1 + red) + 1 + 1 + 1 + (1 + red) + 1 + 1
+    assert mlp.dispatches_por_passo() == 2 * (1 + red) + 1 + 1 + 1 + (1 + red) + 1
     assert loss < 0.01
 
 
@@ -155,23 +157,40 @@ def test_config_batch32_sgd_one_step(gpu):
               [w - p for w, p in zip(mlp.weights(), p0)], 1e-4, 1e-4)
 
 
-@pytest.mark.parametrize("dims,batch,opt,lr", [([512, 1024, 1024, 10], 2048, "adam", 1e-3),
-                                              ([512, 1024, 1024, 10], 32, "sgd", 0.01),
-                                              ([64, 128, 96, 48, 10], 256, "adam", 1e-2)])
-def test_plan_update_is_the_optimizer_entry_point_on_its_gradients(gpu, dims, batch, opt, lr):
-    # An f32 plan runs the update of layers 1.. inside layer 0's dW launch and
-    # layer 0's after it: after one step every weight is, bit for bit,
-    # rt_adam / rt_sgd applied to its initial value and the plan's gradient.
+@pytest.mark.parametrize("dims,batch,opt,lr,in_tiles", [([512, 1024, 1024, 10], 2048, "adam", 1e-3, False),
+                                                       ([512, 1024, 1024, 10], 32, "sgd", 0.01, True),
+                                                       ([512, 1024, 1024, 10], 32, "adam", 1e-3, True),
+                                                       ([512, 1024, 1024, 10], 64, "momentum", 0.01, True),
+                                                       ([64, 128, 96, 48, 10], 256, "adam", 1e-2, None)])
+def test_plan_update_is_the_optimizer_entry_point_on_its_gradients(gpu, dims, batch, opt, lr, in_tiles):
+    # An f32 plan runs the update of layers 1.. inside layer 0's dW launch;
+    # layer 0's update follows in its own launch, or, when that dW is one
+    # unsplit launch (batches up to 128 here), is done by the dW tiles
+    # themselves and the step has no optimizer launch.  Either way, after one
+    # step every weight is, bit for bit, rt_adam / rt_sgd applied to its
+    # initial value and the plan's gradient.
     params = kaiming_model(5, dims)
     x = normal_batch(105, batch, dims[0])
     lab = uniform_labels(106, batch, dims[-1])
-    kw = {"optimizer": "sgd"} if opt == "sgd" else {}
+    kw = {"adam": {}, "sgd": {"optimizer": "sgd"}, "momentum": {"optimizer": "sgd", "momentum": 0.9}}[opt]
     mlp = G.GpuMlp.from_params(gpu, params, batch, lr, **kw)
-    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+    gpu.profile(True)
+    gpu.profile_reset()
+    try:
+        mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+        prof = gpu.perfilar()
+    finally:
+        gpu.profile(False)
+    labels = [name for name, _, _ in prof]
+    if in_tiles is not None:
+        assert ("optimizer" not in labels) == in_tiles, labels
+    assert sum(n for _, n, _ in prof) == mlp.dispatches_por_passo(), prof
     for p0, g, w in zip(params, mlp.grads(), mlp.weights()):
         th = gpu.upload(p0.reshape(w.shape))
         if opt == "adam":
             gpu.adam(th, gpu.zeros(w.shape), gpu.zeros(w.shape), gpu.upload(g), lr, (0.9, 0.999), 1)
+        elif opt == "momentum":
+            gpu.sgd(th, gpu.upload(g), lr, 0.9, velocity=gpu.zeros(w.shape))
         else:
             gpu.sgd(th, gpu.upload(g), lr)
         assert np.array_equal(gpu.download(th).view(np.uint32), w.view(np.uint32)), w.shape
