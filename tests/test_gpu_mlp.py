@@ -196,6 +196,55 @@ def test_plan_update_is_the_optimizer_entry_point_on_its_gradients(gpu, dims, ba
         assert np.array_equal(gpu.download(th).view(np.uint32), w.view(np.uint32)), w.shape
 
 
+def _op_level_grads(gpu, params, x, lab, dims, batch):
+    """One f32 step's gradients from the op-level entry points, one product
+    per launch: forward GEMMs with the bias(+ReLU) epilogue, the softmax
+    cross-entropy, then per layer dW (+ db) by rt_gemm, or by split-K with the
+    plan's slice count, and dX with the ReLU-mask epilogue."""
+    n = len(dims) - 1
+    W = [gpu.upload(params[2 * i]) for i in range(n)]
+    b = [gpu.upload(params[2 * i + 1].reshape(1, -1)) for i in range(n)]
+    acts = [gpu.upload(x)]
+    for l in range(n):
+        h = gpu.zeros((batch, dims[l + 1]))
+        gpu.matmul_bias(acts[-1], W[l], h, b[l], relu=l < n - 1)
+        acts.append(h)
+    d = gpu.zeros((batch, dims[-1]))
+    gpu.softmax_xent(acts[-1], G.upload_labels(gpu, lab), d, gpu.zeros((batch,)))  # δ = (p − y) / batch
+    grads = [None] * (2 * n)
+    for l in reversed(range(n)):
+        dw, db = gpu.zeros((dims[l], dims[l + 1])), gpu.zeros((1, dims[l + 1]))
+        s = G.Gpu.fatias_sugeridas(dims[l], dims[l + 1], batch)
+        if s > 1:
+            part = gpu.zeros((s * (dims[l] * dims[l + 1] + dims[l + 1]),))
+            gpu.split_k(acts[l], d, dw, part, s, True, colsum=db)
+        else:
+            gpu.matmul_at_b(acts[l], d, dw, colsum=db)
+        grads[2 * l], grads[2 * l + 1] = gpu.download(dw), gpu.download(db)
+        if l > 0:
+            dp = gpu.zeros((batch, dims[l]))
+            gpu.matmul_a_bt(d, W[l], dp, relu_mask_from=acts[l])
+            d = dp
+    return grads
+
+
+@pytest.mark.parametrize("dims,batch", [([512, 1024, 1024, 10], 32), ([256, 512, 512, 10], 64),
+                                        ([512, 1024, 1024, 10], 2048)])
+def test_plan_gradients_are_the_op_level_products(gpu, dims, batch):
+    # The plan's fused launches change no bits: the output layer fused with
+    # the loss, the dW+dX pairs (the rank-K dX of the output layer among
+    # them) and the split dW planes summed by the update give, bit for bit,
+    # the gradients of the same products launched one by one.
+    params = kaiming_model(8, dims)
+    x = normal_batch(108, batch, dims[0])
+    lab = uniform_labels(109, batch, dims[-1])
+    mlp = G.GpuMlp.from_params(gpu, params, batch, 1e-3, optimizer="sgd")
+    mlp.step(gpu.upload(x), G.upload_labels(gpu, lab))
+    want = _op_level_grads(gpu, params, x, lab, dims, batch)
+    for i, (g, w) in enumerate(zip(mlp.grads(), want)):
+        assert np.array_equal(g.reshape(-1).view(np.uint32), w.reshape(-1).view(np.uint32)), (i, g.shape)
+
+
 def test_config_batch2048_adam_100_steps(gpu):
     # MLP 512->1024->1024->10 f32 at batch 2048, Adam(1e-3, 0.9, 0.999, 1e-8),
     # 100 steps on fresh seeded N(0,1) batches; per-step loss and final weights.
