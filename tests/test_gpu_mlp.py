@@ -359,6 +359,45 @@ def test_bad_labels_skip_the_update_and_are_reported_once(gpu, precision):
     assert e.value.status == "RT_ERR_SHAPE"
 
 
+@pytest.mark.parametrize("opt", ["adam", "momentum"])
+def test_bad_labels_skip_the_update_done_by_the_dw_tiles(gpu, opt):
+    # A plan whose layer-0 dW tiles update layer 0 themselves (an unsplit
+    # 64x64-tile dW; no optimizer launch): a bad label leaves every weight
+    # and moment unchanged there too, and training then continues as if the
+    # bad step never ran.
+    dims, batch = [64, 64, 64, 4], 64
+    x, lab = quadrant_data(batch, dims[0])
+    params = glorot_model(43, dims)
+    kw = {"adam": {}, "momentum": {"optimizer": "sgd", "momentum": 0.9}}[opt]
+    bad_lab = lab.copy()
+    bad_lab[5] = 4
+    gx, good, bad = gpu.upload(x), G.upload_labels(gpu, lab), G.upload_labels(gpu, bad_lab)
+    mlp = G.GpuMlp.from_params(gpu, params, batch, 0.01, **kw)
+    gpu.profile(True)
+    gpu.profile_reset()
+    try:
+        mlp.step(gx, good)
+        labels = [name for name, _, _ in gpu.perfilar()]
+    finally:
+        gpu.profile(False)
+    assert "optimizer" not in labels, labels
+    w1, (m1, v1, t1) = mlp.weights(), mlp.optimizer_state()
+    mlp.step(gx, bad)
+    with pytest.raises(G.RtError) as e:
+        mlp.last_loss()
+    assert e.value.status == "RT_ERR_LABEL"
+    m2, v2, t2 = mlp.optimizer_state()
+    assert t2 == t1
+    for a, b in zip(w1 + m1 + v1, mlp.weights() + m2 + v2):
+        assert np.array_equal(a, b)
+    mlp.step(gx, good)
+    ref = G.GpuMlp.from_params(gpu, params, batch, 0.01, **kw)
+    ref.step(gx, good)
+    ref.step(gx, good)
+    for a, b in zip(mlp.weights() + list(mlp.optimizer_state()[0]), ref.weights() + list(ref.optimizer_state()[0])):
+        assert np.array_equal(a, b)
+
+
 def test_training_is_deterministic(gpu):
     x, lab = quadrant_data(512, 8)
     params = glorot_model(9, [8, 128, 4])
