@@ -797,6 +797,25 @@ __global__ __launch_bounds__(F32Dma::THREADS) void gemm_f32_opt_upd_kernel(F32Ar
   }
 }
 
+// Two such products (two layers' dW, each updating its own layer) and the
+// optimizer blocks of b in one launch: blocks [0, n0) problem 0 (n0 a
+// multiple of 8, the padding idle), [n0, n1) problem 1, the rest the update.
+__global__ __launch_bounds__(F32Dma::THREADS) void gemm_f32_opt_upd2_kernel(F32Args p0, F32Args p1, rt_opt::OptBatch b,
+                                                                           int n0, int n1, UpdEpi u0, UpdEpi u1) {
+  static_assert(F32Dma::THREADS == rt_opt::kThreads, "one block size");
+  __shared__ __attribute__((aligned(16))) float smem[F32Dma::SMEM];
+  const int blk = blockIdx.x;
+  if (blk < n0) {
+    const int nb = p0.tiles_m * p0.tiles_n;
+    if (blk >= nb) return;  // padding up to a multiple of 8
+    F32Dma::run<false, false>(p0, xcd_local(blk, nb), 0, smem, u0);
+  } else if (blk < n1) {
+    F32Dma::run<false, false>(p1, xcd_local(blk - n0, n1 - n0), 0, smem, u1);
+  } else {
+    rt_opt::optimizer_block<false>(b, blk - n1);
+  }
+}
+
 // The first cs_blocks blocks each take 256 columns of the column sums: they
 // start first, so their chains of loads run under the plane sums; the rest
 // sum the planes (grid-stride over M*N).
@@ -1218,6 +1237,30 @@ hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts
       if (dma_ok<false, false>(a)) return launch_gemm_opt<F32DmaTile<false, false>, 64, 64>(s, a, b, opt_blocks);
       return launch_gemm_opt<F32Tile<64, 64, false, false>, 64, 64>(s, a, b, opt_blocks);
   }
+}
+
+hipError_t gemm_opt_update2_launch(hipStream_t s, const GemmDesc& d0, const OptTensor* upd0, const GemmDesc& d1,
+                                   const OptTensor* upd1, const OptTensor* ts, int nt, const OptParams& P) {
+  if (!gemm_opt_supported(d0, ts, nt, P) || !gemm_opt_update_ok(d0, upd0, P) || !gemm_opt_update_ok(d1, upd1, P))
+    return hipErrorInvalidValue;
+  rt_opt::OptBatch b{};
+  long long opt_blocks = 0;
+  double bytes = 0.0;
+  hipError_t e = rt_opt::make_batch(ts, nt, P, b, &opt_blocks, &bytes);
+  if (e != hipSuccess) return e;
+  F32Args a0 = make_args(d0), a1 = make_args(d1);
+  for (F32Args* a : {&a0, &a1}) {
+    a->tiles_m = a->M / 64;
+    a->tiles_n = a->N / 64;
+  }
+  const long long n0 = ((long long)a0.tiles_m * a0.tiles_n + 7) / 8 * 8;
+  const long long n1 = n0 + (long long)a1.tiles_m * a1.tiles_n;
+  if (n1 + opt_blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  UpdEpi u0{upd0[0], upd0[1], P}, u1{upd1[0], upd1[1], P};
+  u0.P.skip_count = u1.P.skip_count = nullptr;  // counted by the optimizer blocks of the launch
+  rt::launch(gemm_f32_opt_upd2_kernel, dim3((unsigned)(n1 + opt_blocks)), dim3(F32Dma::THREADS), 0, s, a0, a1, b,
+             (int)n0, (int)n1, u0, u1);
+  return hipGetLastError();
 }
 
 bool gemm_pair_supported(const GemmDesc& d0, const GemmDesc& d1) {

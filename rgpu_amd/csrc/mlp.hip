@@ -313,14 +313,14 @@ static bool fuse_update(const rt_mlp* p) {
 }
 
 // Layer 0's W and b as the targets of an update done by its own dW tiles.
-static std::array<OptTensor, 2> layer0_update(const rt_mlp* p, const OptParams& P) {
-  const Layer& L0 = p->L[0];
+static std::array<OptTensor, 2> layer_update(const rt_mlp* p, int l, const OptParams& P) {
+  const Layer& Ly = p->L[l];
   auto seg = [&](size_t off, size_t n) {
     OptTensor T{p->theta + off, p->grad + off, p->m + off, p->v + off, nullptr, n};
     if (P.kind == 1 && P.momentum == 0.0f) T.m = nullptr;
     return T;
   };
-  return {seg(L0.w_off, L0.din * L0.dout), seg(L0.b_off, L0.dout)};
+  return {seg(Ly.w_off, Ly.din * Ly.dout), seg(Ly.b_off, Ly.dout)};
 }
 
 // Layer 0's dW of an f32 plan as one unsplit launch of DMA tiles: with the
@@ -330,15 +330,35 @@ static std::array<OptTensor, 2> layer0_update(const rt_mlp* p, const OptParams& 
 static bool update_in_tiles(const rt_mlp* p, const GemmDesc& dw) {
   if (!fuse_update(p) || p->L[0].dw_parts != nullptr || p->L[0].splits_dw > 1) return false;
   const OptParams P = plan_params(p);
-  return gemm_opt_update_ok(dw, layer0_update(p, P).data(), P);
+  return gemm_opt_update_ok(dw, layer_update(p, 0, P).data(), P);
 }
-// Layer 0's f32 dW launch as the step builds it for the batch x (any 16-byte
-// aligned pointer, nullptr included, gives the step's tile decisions).
-static GemmDesc layer0_dw(rt_mlp* p, const void* x) {
-  const Layer& L0 = p->L[0];
-  return plan_desc(p, RT_TN, RT_F32, x, L0.delta, p->grad + L0.w_off, RT_F32, (int)L0.din, (int)L0.dout,
-                   (int)p->batch, (int)L0.din, (int)L0.ldh, RT_EPI_NONE, nullptr, nullptr, RT_F32,
-                   p->grad + L0.b_off, L0.splits_dw, L0.dw_parts);
+// Layer l's f32 dW launch as the step builds it; in = the layer's input (for
+// layer 0 the batch: any 16-byte aligned pointer, nullptr included, gives
+// the step's tile decisions).
+static GemmDesc f32_dw(rt_mlp* p, int l, const void* in) {
+  const Layer& Ly = p->L[l];
+  return plan_desc(p, RT_TN, RT_F32, in, Ly.delta, p->grad + Ly.w_off, RT_F32, (int)Ly.din, (int)Ly.dout,
+                   (int)p->batch, (int)Ly.din, (int)Ly.ldh, RT_EPI_NONE, nullptr, nullptr, RT_F32,
+                   p->grad + Ly.b_off, Ly.splits_dw, Ly.dw_parts);
+}
+static GemmDesc layer0_dw(rt_mlp* p, const void* x) { return f32_dw(p, 0, x); }
+
+// Layer 1's dW joins layer 0's launch as well (f32 plans of 3+ layers whose
+// layer 0 is updated by its dW tiles, and whose layer 1 runs its dW alone,
+// unsplit, on the same tiles): those tiles update layer 1, the launch's
+// optimizer blocks take layers 2.., and the step has one launch fewer.
+// Layer 1's dW reads only δ₁ and the layer's input, which its dX launch
+// before it does not change.
+static bool fold_l1(rt_mlp* p, const void* x) {
+  if (p->mixed || p->n_layers < 3) return false;
+  const Layer& L1 = p->L[1];
+  if (L1.pair_bwd || L1.splits_dw > 1 || L1.dw_parts != nullptr || !update_in_tiles(p, layer0_dw(p, x)))
+    return false;
+  const OptParams P = plan_params(p);
+  const std::vector<OptTensor> rest = plan_tensors(p, 2, p->n_layers, P);
+  return !rest.empty() && (int)rest.size() <= kMaxOptTensors &&
+         optimizer_fits_cache(rest.data(), (int)rest.size(), P) &&
+         gemm_opt_update_ok(f32_dw(p, 1, p->L[0].act), layer_update(p, 1, P).data(), P);
 }
 
 // Optimizer launches after the backward: none when layer 0's dW tiles do
@@ -590,11 +610,12 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   p->head_fused = !p->mixed && head_xent_supported((int)top.din, (int)top.dout);
 
   // Launch count of one step.
+  const bool fold = fold_l1(p, nullptr);
   int n = 0;
   for (int l = 0; l < n_layers; ++l) {
     const bool fused = l == n_layers - 1 && p->head_fused;
     n += fused ? 1 : (p->L[l].splits_fwd > 1 ? 2 : 1);
-    n += (p->L[l].splits_dw > 1 && !p->L[l].dw_parts) ? 2 : 1;
+    if (!(fold && l == 1)) n += (p->L[l].splits_dw > 1 && !p->L[l].dw_parts) ? 2 : 1;
     if (p->mixed) {  // the dW GEMM's shares are added elsewhere: one launch
       const Layer& Ly = p->L[l];
       const void* a_in = l == 0 ? nullptr : p->L[l - 1].act;
@@ -693,6 +714,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
   const bool fuse = fuse_update(p);
   bool fused = false;  // layers 1..'s update ran in layer 0's dW launch
   bool upd0 = false;   // and layer 0's in that launch's tiles
+  const bool fold = fold_l1(p, x->ptr);  // layer 1's dW (and update) in that launch too
 
   const int in_dtype = p->mixed ? RT_BF16 : RT_F32;
   std::vector<char> unchecked(nl, 1);
@@ -718,14 +740,21 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       if (rows > 0) jobs.push_back(ShareJob{Ly.cs_shares, p->grad + Ly.b_off, rows, (int)Ly.dout});
     }
     if (l == 0) {
-      const std::vector<OptTensor> rest = fuse ? plan_tensors(p, 1, nl, P) : std::vector<OptTensor>();
+      const std::vector<OptTensor> rest = fuse ? plan_tensors(p, fold ? 2 : 1, nl, P) : std::vector<OptTensor>();
       if (fuse && gemm_opt_supported(dw, rest.data(), (int)rest.size(), P)) {
         OptParams Pr = P;
         Pr.skip_count = p->state + 4;
         upd0 = update_in_tiles(p, dw);
-        const std::array<OptTensor, 2> wb = layer0_update(p, P);
+        const std::array<OptTensor, 2> wb = layer_update(p, 0, P);
         Launch Lz(c, Ly.lbl_dw.c_str());
-        hipError_t e = gemm_opt_launch(c->stream, dw, rest.data(), (int)rest.size(), Pr, upd0 ? wb.data() : nullptr);
+        hipError_t e;
+        if (fold) {
+          const std::array<OptTensor, 2> wb1 = layer_update(p, 1, P);
+          e = gemm_opt_update2_launch(c->stream, dw, wb.data(), f32_dw(p, 1, Ly.act), wb1.data(), rest.data(),
+                                      (int)rest.size(), Pr);
+        } else {
+          e = gemm_opt_launch(c->stream, dw, rest.data(), (int)rest.size(), Pr, upd0 ? wb.data() : nullptr);
+        }
         if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());
         fused = true;
       } else {
@@ -749,7 +778,7 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
         hipError_t e = gemm_pair_launch(c->stream, dw, dx);
         if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_bwd.c_str());
       } else {
-        {
+        if (!(fold && l == 1)) {  // under fold_l1 it runs in layer 0's dW launch
           Launch Lz(c, Ly.lbl_dw.c_str());
           hipError_t e = gemm_launch(c->stream, dw);
           if (e != hipSuccess) return hip_fail(c, e, Ly.lbl_dw.c_str());

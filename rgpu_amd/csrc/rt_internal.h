@@ -291,6 +291,10 @@ bool gemm_opt_supported(const GemmDesc& d, const OptTensor* ts, int nt, const Op
 bool gemm_opt_update_ok(const GemmDesc& d, const OptTensor* wb, const OptParams& p);
 hipError_t gemm_opt_launch(hipStream_t s, const GemmDesc& d, const OptTensor* ts, int nt, const OptParams& p,
                            const OptTensor* upd = nullptr);
+// Two unsplit TN dW products, each with its {W, b} update done by its tiles
+// (both gemm_opt_update_ok), and the update of ts, in one launch.
+hipError_t gemm_opt_update2_launch(hipStream_t s, const GemmDesc& d0, const OptTensor* upd0, const GemmDesc& d1,
+                                   const OptTensor* upd1, const OptTensor* ts, int nt, const OptParams& p);
 // Column sums of a whole (unsplit) half GEMM left as shares: dst[j] = the
 // rows src[t * n + j], t = 0 .. rows-1, added in order from zero (what the
 // GEMM's own shares launch computes).

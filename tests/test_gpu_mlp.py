@@ -110,12 +110,12 @@ def test_small_batch_plan_follows_cpu(gpu, batch, dims, steps):
         assert min(s_fwd) > 1 and s_dx > 1, "the hidden forward and dX GEMMs must be split"
     loss, mlp = _trajectory(gpu, x, lab, dims, 3, steps, 1e-3)
     # Launches: the 2 hidden forwards (each + its reduction when split), the
-    # fused head and loss, the head's dW+dX pair, layer 1's dW and dX (+ its
-    # reduction when split), layer 0's dW, whose launch also updates layers
-    # 1.. and whose tiles update layer 0 (its K of at most 96 is not split):
-    # no optimizer launch.
+    # fused head and loss, the head's dW+dX pair, layer 1's dX (+ its
+    # reduction when split), and layer 0's dW, whose launch also computes
+    # layer 1's dW (both unsplit at K <= 96), its tiles updating layers 0
+    # and 1, and the head's update: no optimizer launch.
     red = 0 if skinny[0] else 1
-    assert mlp.dispatches_por_passo() == 2 * (1 + red) + 1 + 1 + 1 + (1 + red) + 1
+    assert mlp.dispatches_por_passo() == 2 * (1 + red) + 1 + 1 + (1 + red) + 1
     assert loss < 0.01
 
 
@@ -166,9 +166,11 @@ def test_plan_update_is_the_optimizer_entry_point_on_its_gradients(gpu, dims, ba
     # An f32 plan runs the update of layers 1.. inside layer 0's dW launch;
     # layer 0's update follows in its own launch, or, when that dW is one
     # unsplit launch (batches up to 128 here), is done by the dW tiles
-    # themselves and the step has no optimizer launch.  Either way, after one
-    # step every weight is, bit for bit, rt_adam / rt_sgd applied to its
-    # initial value and the plan's gradient.
+    # themselves and the step has no optimizer launch (then an unsplit
+    # layer-1 dW that is not paired with its dX joins that launch and
+    # updates layer 1 the same way).  Either way, after one step every
+    # weight is, bit for bit, rt_adam / rt_sgd applied to its initial value
+    # and the plan's gradient.
     params = kaiming_model(5, dims)
     x = normal_batch(105, batch, dims[0])
     lab = uniform_labels(106, batch, dims[-1])
