@@ -161,6 +161,7 @@ def test_config_batch32_sgd_one_step(gpu):
                                                        ([512, 1024, 1024, 10], 32, "sgd", 0.01, True),
                                                        ([512, 1024, 1024, 10], 32, "adam", 1e-3, True),
                                                        ([512, 1024, 1024, 10], 64, "momentum", 0.01, True),
+                                                       ([256, 512, 256, 128, 10], 32, "adam", 1e-3, True),
                                                        ([64, 128, 96, 48, 10], 256, "adam", 1e-2, None)])
 def test_plan_update_is_the_optimizer_entry_point_on_its_gradients(gpu, dims, batch, opt, lr, in_tiles):
     # An f32 plan runs the update of layers 1.. inside layer 0's dW launch;
@@ -231,7 +232,7 @@ def _op_level_grads(gpu, params, x, lab, dims, batch):
 
 
 @pytest.mark.parametrize("dims,batch", [([512, 1024, 1024, 10], 32), ([256, 512, 512, 10], 64),
-                                        ([512, 1024, 1024, 10], 2048)])
+                                        ([256, 512, 256, 128, 10], 32), ([512, 1024, 1024, 10], 2048)])
 def test_plan_gradients_are_the_op_level_products(gpu, dims, batch):
     # The plan's fused launches change no bits: the output layer fused with
     # the loss, the dW+dX pairs (the rank-K dX of the output layer among
