@@ -745,31 +745,44 @@ struct UpdEpi {
     const bool skip = rt_opt::skipped(P);
     const rt_opt::Coef c = rt_opt::coef(P);
     const bool adam = P.kind == 0, has_m = w.m != nullptr;
+    long long idx[2][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const long long row_off = (long long)(m0 + wm + 16 * t + r) * p.ldc;
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) idx[t][u] = (long long)(m0 + wm + 16 * t + r) * p.ldc + n0 + wn + 16 * u + 4 * g;
+    // Every load of θ and the state first, so that they go out together
+    // (the stores below could alias them as far as the compiler knows).
+    f4 th[2][2], m[2][2], v[2][2];
+    if (!skip) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          th[t][u] = *reinterpret_cast<const f4*>(w.theta + idx[t][u]);
+          m[t][u] = has_m ? *reinterpret_cast<const f4*>(w.m + idx[t][u]) : f4{0, 0, 0, 0};
+          v[t][u] = adam ? *reinterpret_cast<const f4*>(w.v + idx[t][u]) : f4{0, 0, 0, 0};
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const long long i = row_off + n0 + wn + 16 * u + 4 * g;
+        const long long i = idx[t][u];
         const f4 gv = acc[t][u];
         *reinterpret_cast<f4*>(p.C + i) = gv;
         if (skip) continue;
-        f4 th = *reinterpret_cast<const f4*>(w.theta + i);
-        f4 m = has_m ? *reinterpret_cast<const f4*>(w.m + i) : f4{0, 0, 0, 0};
-        f4 v = adam ? *reinterpret_cast<const f4*>(w.v + i) : f4{0, 0, 0, 0};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          float te = th[q], me = m[q], ve = v[q];
+          float te = th[t][u][q], me = m[t][u][q], ve = v[t][u][q];
           rt_opt::update(P, c, gv[q], te, &me, &ve);
-          th[q] = te;
-          m[q] = me;
-          v[q] = ve;
+          th[t][u][q] = te;
+          m[t][u][q] = me;
+          v[t][u][q] = ve;
         }
-        *reinterpret_cast<f4*>(w.theta + i) = th;
-        if (has_m) *reinterpret_cast<f4*>(w.m + i) = m;
-        if (adam) *reinterpret_cast<f4*>(w.v + i) = v;
+        *reinterpret_cast<f4*>(w.theta + i) = th[t][u];
+        if (has_m) *reinterpret_cast<f4*>(w.m + i) = m[t][u];
+        if (adam) *reinterpret_cast<f4*>(w.v + i) = v[t][u];
       }
-    }
   }
   __device__ void bias(const F32Args& p, int col, float gv) const {
     p.colsum[col] = gv;
