@@ -640,20 +640,30 @@ struct F32RankK {
     float* sb = smem + 64 * LD;
     const int tile_m = bid / p.tiles_n, tile_n = bid - tile_m * p.tiles_n;
     const int m0 = 64 * tile_m, n0 = 64 * tile_n, K = p.K, tid = threadIdx.x;
+    const int r0 = 4 * (tid / 16), c0 = 4 * (tid % 16);
+    const int col = n0 + c0;
+    // The ReLU mask of this thread's outputs, loaded first so that its
+    // latency runs under the operand staging and the multiply-adds.
+    const bool vec_mask = p.epi == RT_EPI_RELU_MASK && p.vec_c && col + 4 <= p.N;
+    f4 mkv[4];
+    if (vec_mask) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        mkv[i] = m0 + r0 + i < p.M ? *reinterpret_cast<const f4*>(p.mask + (long long)(m0 + r0 + i) * p.ldc + col)
+                                   : f4{0, 0, 0, 0};
+    }
     for (int i = tid; i < 64 * K; i += THREADS) {
       const int r = i / K, k = i - r * K;
       sa[r * LD + k] = m0 + r < p.M ? p.A[(long long)(m0 + r) * p.lda + k] : 0.0f;
       sb[r * LD + k] = n0 + r < p.N ? p.B[(long long)(n0 + r) * p.ldb + k] : 0.0f;
     }
     __syncthreads();
-    const int r0 = 4 * (tid / 16), c0 = 4 * (tid % 16);
     f4 acc[4] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}, f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
     for (int k = 0; k < K; ++k) {
       const f4 b = f4{sb[c0 * LD + k], sb[(c0 + 1) * LD + k], sb[(c0 + 2) * LD + k], sb[(c0 + 3) * LD + k]};
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[i] += sa[(r0 + i) * LD + k] * b;
     }
-    const int col = n0 + c0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = m0 + r0 + i;
@@ -666,10 +676,9 @@ struct F32RankK {
           v += *reinterpret_cast<const f4*>(p.bias + col);
           if (p.epi == RT_EPI_BIAS_RELU)
             for (int q = 0; q < 4; ++q) v[q] = fmaxf(v[q], 0.0f);
-        } else if (p.epi == RT_EPI_RELU_MASK) {
-          const f4 m = *reinterpret_cast<const f4*>(mk);
+        } else if (vec_mask) {
           for (int q = 0; q < 4; ++q)
-            if (!(m[q] > 0.0f)) v[q] = 0.0f;
+            if (!(mkv[i][q] > 0.0f)) v[q] = 0.0f;
         }
         *reinterpret_cast<f4*>(c) = v;
       } else {
