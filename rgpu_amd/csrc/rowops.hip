@@ -123,6 +123,15 @@ __global__ __launch_bounds__(64 * HW) void head_xent_kernel(const float* __restr
   const int nch = kq / 16;     // chunks of 16 k per wave
   const int kw = wave * kq;
   const float* arow = A + (long long)min(r0 + r, rows - 1) * K + kw + 4 * g;  // rows past the end read the last row
+  // The softmax lanes' label and bias, loaded first so that their latency
+  // runs under the K loop.
+  uint32_t ylab = 0;
+  float bv = 0.0f;
+  if (threadIdx.x < HEAD_ROWS * HEAD_C) {
+    const int row = r0 + (int)(threadIdx.x >> 4), cc = threadIdx.x & 15;
+    if (labels != nullptr && row < rows) ylab = labels[row];
+    if (bias != nullptr && cc < cols) bv = bias[cc];
+  }
   f4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int c0 = 0; c0 < nch; c0 += 8) {
     f4v av[8];
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(64 * HW) void head_xent_kernel(const float* __restr
   float zs = red[0][rr][cc];
 #pragma unroll
   for (int w = 1; w < HW; ++w) zs += red[w][rr][cc];
-  const float z = cc < cols ? (bias != nullptr ? zs + bias[cc] : zs) : -INFINITY;
+  const float z = cc < cols ? (bias != nullptr ? zs + bv : zs) : -INFINITY;
   if (row >= rows) return;
   if (cc < cols) logits[(long long)row * cols + cc] = z;
   if (labels == nullptr) return;
@@ -167,7 +176,7 @@ __global__ __launch_bounds__(64 * HW) void head_xent_kernel(const float* __restr
   float sum = e;
 #pragma unroll
   for (int off = 8; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 16);
-  const uint32_t y = labels[row];
+  const uint32_t y = ylab;
   const bool bad = y >= (uint32_t)cols;
   if (bad && cc == 0) {
     *err_flag = 1;
