@@ -335,6 +335,102 @@ def test_div_vjp_matches_float64_and_numeric(sa, sb):  # ops.rs:93-102
     _numeric_check([pa, pb], [ga, gb], lambda: build(O.Tape()).item(), h=1e-2)
 
 
+def test_neg_value_and_vjp_are_sign_flips():  # ops.rs:145-147 (neg = scale by -1)
+    # every finite class, both zeros, subnormals and infinities: -x is a sign-bit flip
+    x = np.array([[0.0, -0.0, 1.5, -2.25, 1e-40, -1e-40, 3.4e38, np.inf, -np.inf, 7.0]], np.float32)
+    w = np.array([[1.0, -2.0, 0.5, 3.0, -1e-39, 4.0, -0.0, 2.0, 8.0, 1e30]], np.float32)
+    p = O.Param(x)
+    t = O.Tape()
+    y = t.watch(p).neg()
+    y.mul(t.constant(w)).sum().backward()
+    flip = np.uint32(0x80000000)
+    assert np.array_equal(y.value().view(np.uint32), x.view(np.uint32) ^ flip)
+    # the VJP is -g: a VJP that passed g through, or scaled by |k|, fails here
+    assert np.array_equal(t.grad(p).view(np.uint32), w.view(np.uint32) ^ flip)
+    # neg twice is the identity, value and gradient
+    p2 = O.Param(x[:, :7])
+    t2 = O.Tape()
+    y2 = t2.watch(p2).neg().neg()
+    y2.mul(t2.constant(w[:, :7])).sum().backward()
+    assert np.array_equal(y2.value().view(np.uint32), x[:, :7].view(np.uint32))
+    assert np.array_equal(t2.grad(p2).view(np.uint32), w[:, :7].view(np.uint32))
+
+
+# Shape pairs of the N-D broadcast paths: tensor.rs:183-246 (zip: tiled,
+# column and generic strided paths) and 399-438 (reduce_to: tiled, column and
+# generic paths), at rank 3 and 4, with broadcasts on leading, middle and
+# trailing axes and on both operands at once.
+_ND_PAIRS = [
+    ((2, 3, 4), (3, 1)), ((2, 1, 4), (1, 3, 1)), ((5,), (2, 1, 5)), ((2, 3, 4, 5), (3, 1, 5)),
+    ((2, 3, 4), (2, 3, 4)), ((2, 3, 4), (4,)), ((2, 3, 4), (1, 3, 1)), ((1, 3, 1, 5), (2, 3, 4, 5)),
+    ((2, 1, 4, 1), (1, 3, 1, 5)), ((3, 1), (2, 3, 4)),
+]
+_NUMPY_OP = {"add": np.add, "sub": np.subtract, "mul": np.multiply, "div": np.divide}
+
+
+@pytest.mark.parametrize("sa,sb", _ND_PAIRS)
+def test_zip_nd_broadcast_matches_numpy_bitwise(sa, sb):
+    # numpy's float32 +, -, *, / round once, as the reference's f(a, b) does;
+    # numpy broadcasting is an independent statement of which a[.] meets which b[.]
+    rng = np.random.default_rng(len(sa) * 7 + len(sb))
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    b = np.where(np.abs(b) < 0.1, np.float32(0.5), b).astype(np.float32)
+    for op, f in _NUMPY_OP.items():
+        t = O.Tape()
+        got = getattr(t.constant(a), op)(t.constant(b)).value()
+        want = f(a, b)
+        assert got.shape == want.shape, (op, got.shape, want.shape)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), op
+
+
+def _reduce_to_by_tape(g, target):
+    # the oracle's reduce_to at any rank: the VJP of p + 0 (p of the target
+    # shape) for the upstream gradient g
+    p = O.Param(np.zeros(target, np.float32))
+    t = O.Tape()
+    t.watch(p).add(t.constant(np.zeros(g.shape, np.float32))).mul(t.constant(g)).sum().backward()
+    return t.grad(p)
+
+
+def _reduce_to_in_source_order(g, target):
+    # out[j] accumulates G[l] for increasing linear source index l, in f32:
+    # iterate the summed axes lexicographically and add whole slices
+    lead = g.ndim - len(target)
+    tgt = (1,) * lead + tuple(target)
+    summed = [ax for ax in range(g.ndim) if tgt[ax] == 1 and g.shape[ax] != 1]
+    out = np.zeros(tgt, np.float32)
+    for idx in np.ndindex(*[g.shape[ax] for ax in summed]):
+        sl = [slice(None)] * g.ndim
+        for ax, i in zip(summed, idx):
+            sl[ax] = slice(i, i + 1)
+        out = (out + g[tuple(sl)]).astype(np.float32)
+    return out.reshape(target)
+
+
+@pytest.mark.parametrize("gshape,target", [
+    ((2, 3, 4), (1, 3, 1)), ((2, 3, 4), (2, 1, 4)), ((2, 3, 4), (3, 4)), ((2, 3, 4), (4,)),
+    ((2, 3, 4), (3, 1)), ((2, 3, 4, 5), (1, 3, 1, 5)), ((2, 3, 4, 5), (3, 1, 5)),
+    ((2, 3, 4, 5), (2, 1, 4, 1)), ((2, 3, 4, 5), (1, 1, 1, 1)), ((3, 5, 7, 2), (5, 1, 2)),
+])
+def test_reduce_to_nd_matches_numpy(gshape, target):
+    rng = np.random.default_rng(int(np.prod(gshape)) + len(target))
+    # integers: every summation order gives the exact sum, so numpy's sum over
+    # the broadcast axes pins which entries land where
+    gi = rng.integers(-50, 50, gshape).astype(np.float32)
+    lead = len(gshape) - len(target)
+    tgt = (1,) * lead + tuple(target)
+    axes = tuple(ax for ax in range(len(gshape)) if tgt[ax] == 1 and gshape[ax] != 1)
+    assert np.array_equal(_reduce_to_by_tape(gi, target), gi.sum(axis=axes, keepdims=True).reshape(target))
+    # reals: the order is increasing source index (tensor.rs:399-438), so an
+    # f32 accumulation in that order matches to the bit
+    g = rng.standard_normal(gshape).astype(np.float32)
+    got = _reduce_to_by_tape(g, target)
+    assert np.array_equal(got.view(np.uint32), _reduce_to_in_source_order(g, target).view(np.uint32))
+    want64 = g.astype(np.float64).sum(axis=axes, keepdims=True).reshape(target)
+    assert np.allclose(got, want64, rtol=0, atol=1e-5 * np.abs(g).sum())
+
+
 def test_mae_gradient_closed_form_subgradient_and_upstream():  # losses.rs:46-53
     rng = np.random.default_rng(47)
     pred = rng.normal(size=(4, 3)).astype(np.float32)
