@@ -16,8 +16,8 @@ import pytest
 
 from oracle import oracle as O
 from rgpu_amd import gpu as G
-from tests.gpu_common import (bf16_pipeline_grads, bf16_plan_layer_checks, grad_gate, kaiming_model, normal_batch,
-                              oracle_threads, uniform_labels)
+from tests.gpu_common import (bf16_pipeline_grads, bf16_pipeline_loss, bf16_plan_layer_checks, grad_gate,
+                              kaiming_model, normal_batch, oracle_threads, uniform_labels)
 
 pytestmark = pytest.mark.gpu
 
@@ -69,7 +69,7 @@ def test_splitk_dw_f16(gpu, K, slices):
 
 
 def bf16_gates(mlp, cpu, params_r, x, lab, col_frac=None, emu_bound=None):
-    """Step-1 gradient gates of the bf16 plan.
+    """Gradient gates of one step of the bf16 plan.
 
     1. Layer-local: every GEMM and rounding point of the step on the plan's
        own stored inputs, per element against float64 (pins the kernels).
@@ -79,13 +79,18 @@ def bf16_gates(mlp, cpu, params_r, x, lab, col_frac=None, emu_bound=None):
        layers' gradients up to ~12% norm-wise from f32; the float64
        restatement of the bf16 pipeline measures that inherent distance for
        each tensor, and the plan may deviate from f32 by at most
-       max(2e-2, 2 x) it.  A zeroed or wrong tensor scores ~1.
+       max(2e-2, 2 x) it.  A zeroed or wrong tensor scores ~1.  erro_rel
+       (tests/gpu.rs:53-60) is gated the same way: it is an absolute error
+       while gradients are far below 1, so the 2e-2 floor decides at step 0,
+       but in the loss spike of the 8 x 4096 model (step 1: loss 26) the
+       gradients are O(1) and the restatement itself is up to ~0.19 from f32
+       on it.
     3. Optionally (small widths, where f32-vs-float64 accumulation does not
        flip masks) norm-wise against that restatement itself."""
     gg, gc = mlp.grads(), cpu.grads()
     bf16_plan_layer_checks(mlp, params_r, x, lab, 1024.0)
     emu = bf16_pipeline_grads(params_r, x, lab, col_frac=col_frac)
-    inh_n, inh_m = [], []
+    inh_n, inh_m, inh_e = [], [], []
     for i, (e, c) in enumerate(zip(emu, gc)):
         if isinstance(e, tuple):
             e, cols = e
@@ -93,10 +98,11 @@ def bf16_gates(mlp, cpu, params_r, x, lab, col_frac=None, emu_bound=None):
         c = c.astype(np.float64)
         inh_n.append(float(np.linalg.norm(e - c) / np.linalg.norm(c)))
         inh_m.append(float(np.abs(e - c).max() / np.abs(c).max()))
+        inh_e.append(O.erro_rel(c, e))
     print("inherent bf16 distance from f32 (float64 restatement): norm-wise", ["%.1e" % v for v in inh_n],
-          "\n  max-relative", ["%.1e" % v for v in inh_m], flush=True)
-    grad_gate("bf16 step-1 grads vs the f32 oracle", gc, gg, [max(2e-2, 2 * v) for v in inh_n],
-              [max(2e-2, 2 * v) for v in inh_m], erro_bound=2e-2)
+          "\n  max-relative", ["%.1e" % v for v in inh_m], "\n  erro_rel", ["%.1e" % v for v in inh_e], flush=True)
+    grad_gate("bf16 grads vs the f32 oracle", gc, gg, [max(2e-2, 2 * v) for v in inh_n],
+              [max(2e-2, 2 * v) for v in inh_m], erro_bound=[max(2e-2, 2 * v) for v in inh_e])
     if emu_bound is not None:
         ne = [float(np.linalg.norm(a - b) / max(np.linalg.norm(a), 1e-30)) for a, b in zip(emu, gg)]
         print("  norm-wise vs the bf16 restatement", ["%.1e" % r for r in ne], flush=True)
@@ -156,49 +162,159 @@ def test_mixed_precision_mlp_full_size_step(gpu):
     assert max(d) < 2e-2
 
 
-def test_mixed_precision_mlp_full_size_100_step_trajectory(gpu):
-    """tests/golden/c5_trajectory.json holds the oracle's f32 losses of 100
-    Adam steps of the 8 x 4096 -> 1000 MLP at batch 4096 from bf16-rounded
-    weights and inputs (written by make_c5_trajectory.py beside it), and the
-    losses of two independent numpy restatements of the bf16 plan (float32
-    and float64 accumulation).  The bf16 plan (f32 master weights, loss scale
-    1024) runs the same 100 steps; every loss must stay within max(2e-2, 2 x
-    the farther restatement's distance from the oracle at that step) of the
-    oracle's (the tests/gpu.rs:99-139 pattern at the bf16 bar).  The bound
-    exceeds 2e-2 only in the early loss spike (steps 1-3), where valid bf16
-    implementations land several percent apart."""
-    import concurrent.futures as cf
+SPIKE = (1, 2, 3)  # the loss spike of the 8 x 4096 -> 1000 trajectory (7.96 -> 26.0 -> 13.8 -> 7.3)
+
+
+def _c5_fixture():
     import json
     import os
     from tests.golden import make_c5_trajectory as mk
 
     with open(os.path.join(os.path.dirname(mk.__file__), "c5_trajectory.json")) as f:
         fix = json.load(f)
-    want = [float(np.uint32(b).view(np.float32)) for b in fix["loss_bits"]]
+    want_bits = [int(b) for b in fix["loss_bits"]]
     rest = [fix["bf16_restatement_f32_acc"], fix["bf16_restatement_f64_acc"]]
-    assert len(want) == mk.STEPS and all(len(r) == mk.STEPS for r in rest)
-    bound = [max(2e-2, 2 * max(abs(r[s] - want[s]) / abs(want[s]) for r in rest)) for s in range(mk.STEPS)]
-    mlp = G.GpuMlp.from_params(gpu, mk.initial_params(), mk.BATCH, mk.LR, precision="bf16", loss_scale=1024.0)
+    assert len(want_bits) == mk.STEPS and all(len(r) == mk.STEPS for r in rest)
+    return mk, want_bits, rest
+
+
+def _f32(bits):
+    return float(np.uint32(bits).view(np.float32))
+
+
+def _spike_loss_gate(tag, s, plan, oracle, restated):
+    """The loss of one spike step from a shared state.  The float64
+    restatement of the bf16 pipeline from that state measures how far bf16
+    storage alone moves the loss from f32 (in the spike the logits are large:
+    2.6% at step 2).  The plan must be within 2e-2 of that restatement, and
+    within max(2e-2, 2 x the restatement's own distance) of the f32 oracle."""
+    d_re = abs(plan - restated) / abs(restated)
+    inh = abs(restated - oracle) / abs(oracle)
+    d_or = abs(plan - oracle) / abs(oracle)
+    print(f"{tag} step {s}: oracle {oracle:.5f}, bf16 plan {plan:.5f}, float64 bf16 restatement {restated:.5f}; "
+          f"plan vs restatement {d_re:.2e}, plan vs oracle {d_or:.2e} (restatement vs oracle {inh:.2e})",
+          flush=True)
+    assert d_re <= 2e-2, (tag, s, plan, restated)
+    assert d_or <= max(2e-2, 2 * inh), (tag, s, plan, oracle, inh)
+    return d_re, d_or, inh
+
+
+def test_mixed_precision_mlp_full_size_teacher_forced_spike(gpu):
+    """Steps 1-3 of the 8 x 4096 -> 1000 trajectory at batch 4096 (the loss
+    spike), each started from the oracle's own state: before step s the
+    oracle's f32 weights and Adam m, v, t after s updates are loaded into the
+    bf16 plan (rt_mlp_set_weights, rt_mlp_set_optimizer_state), and the plan's
+    step s on the same batch is checked against the oracle's step s:
+    * the loss within 2e-2 of the float64 restatement of the bf16 pipeline
+      from the same state, and within max(2e-2, 2 x that restatement's
+      distance) of the oracle's (_spike_loss_gate);
+    * every GEMM and rounding point of the step layer-locally against float64
+      on the plan's own stored inputs;
+    * the gradients against the oracle's, whole and scale-aware, within
+      max(2e-2, 2 x the distance bf16 storage alone causes, from the float64
+      restatement of the bf16 pipeline from the same state);
+    * the update used the loaded state: m' = β1·m + (1 − β1)·g and
+      v' = β2·v + (1 − β2)·g² in f32 on the plan's own g, to the bit, and t.
+    With the state shared, the ~100x amplification of earlier differences that
+    a free-running comparison meets in these steps (tests/gpu.rs:99-139
+    compares free-running trajectories) is taken out.  The oracle's losses
+    reproduce the committed fixture's bits."""
+    mk, want_bits, _ = _c5_fixture()
+    params = mk.initial_params()
+    cpu = O.CpuMlp(params[0::2], params[1::2])
+    cpu.set_optimizer("adam", mk.LR)
+    mlp = G.GpuMlp.from_params(gpu, params, mk.BATCH, mk.LR, precision="bf16", loss_scale=1024.0)
+    b1, b2 = np.float32(0.9), np.float32(0.999)
     t0 = time.time()
-    got = []
+    x, lab = mk.batch(0)
+    lc = cpu.step(x, lab)
+    assert int(np.float32(lc).view(np.uint32)) == want_bits[0]
+    for s in SPIKE:
+        x, lab = mk.batch(s)
+        w_s = cpu.weights()
+        m_s, v_s, t_s = cpu.optimizer_state()
+        assert t_s == s
+        mlp.set_weights(w_s)
+        mlp.set_optimizer_state(m_s, v_s, t_s)
+        mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, lab))
+        lg = mlp.last_loss()
+        lc = cpu.step(x, lab)
+        assert int(np.float32(lc).view(np.uint32)) == want_bits[s], (s, lc, _f32(want_bits[s]))
+        _spike_loss_gate("teacher-forced", s, lg, lc, bf16_pipeline_loss(w_s, x, lab))
+        assert not mlp.overflow()
+        bf16_gates(mlp, cpu, w_s, x, lab)
+        g = mlp.grads()
+        m1, v1, t1 = mlp.optimizer_state()
+        assert t1 == s + 1
+        for i in range(len(g)):
+            gi = g[i].astype(np.float32)
+            want_m = (b1 * m_s[i] + (np.float32(1) - b1) * gi).astype(np.float32)
+            want_v = (b2 * v_s[i] + (np.float32(1) - b2) * (gi * gi)).astype(np.float32)
+            assert np.array_equal(m1[i], want_m), (s, i)
+            assert np.array_equal(v1[i], want_v), (s, i)
+        print(f"  step {s}: gates passed ({time.time() - t0:.0f} s)", flush=True)
+
+
+def test_mixed_precision_mlp_full_size_100_step_trajectory(gpu):
+    """tests/golden/c5_trajectory.json holds the oracle's f32 losses of 100
+    Adam steps of the 8 x 4096 -> 1000 MLP at batch 4096 from bf16-rounded
+    weights and inputs (written by make_c5_trajectory.py beside it).  The
+    bf16 plan (f32 master weights, loss scale 1024) runs the same 100 steps
+    free, as tests/gpu.rs:99-139 runs its trajectories, and every loss must
+    stay within 2e-2 of the oracle's, except in the loss spike (steps 1-3).
+
+    There the spike amplifies earlier differences ~100x: two independent
+    numpy restatements of the bf16 plan (in the fixture) land up to 7.9% from
+    the oracle at step 2, and the plan 11.7%.  Each spike step is checked
+    from a shared state instead, from both sides:
+    * from the oracle's state: test_..._teacher_forced_spike above;
+    * from the plan's own state: before step s the plan's weights and Adam
+      m, v, t are loaded into a second oracle, and the plan's step-s loss
+      passes _spike_loss_gate against that oracle's loss and the float64
+      bf16 restatement's from the same weights.
+    So each spike loss is the right function of its state, and the
+    free-running gap there is the difference of states, not of arithmetic."""
+    import concurrent.futures as cf
+
+    mk, want_bits, rest = _c5_fixture()
+    want = [_f32(b) for b in want_bits]
+    params = mk.initial_params()
+    mlp = G.GpuMlp.from_params(gpu, params, mk.BATCH, mk.LR, precision="bf16", loss_scale=1024.0)
+    rev = O.CpuMlp(params[0::2], params[1::2])  # the oracle run from the plan's state
+    rev.set_optimizer("adam", mk.LR)
+    t0 = time.time()
+    got, rev_d = [], {}
     with cf.ThreadPoolExecutor(8) as ex:  # the Rng fills run in C, outside the GIL
         futs = [ex.submit(mk.batch, s) for s in range(mk.STEPS)]
         for s, fu in enumerate(futs):
             x, lab = fu.result()
+            if s in SPIKE:
+                m, v, t = mlp.optimizer_state()
+                assert t == s
+                w_s = mlp.weights()
+                rev.set_weights(w_s)
+                rev.set_optimizer_state(m, v, t)
+                lr_ = rev.step(x, lab)
             mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, lab))
             got.append(mlp.last_loss())
             futs[s] = None
-            if s < 6 or s % 10 == 0:
+            if s in SPIKE:
                 print(f"step {s}: oracle {want[s]:.5f} bf16 {got[-1]:.5f} (restatements {rest[0][s]:.5f}, "
-                      f"{rest[1][s]:.5f}; bound {bound[s]:.1e}) ({time.time() - t0:.0f} s)", flush=True)
+                      f"{rest[1][s]:.5f}) ({time.time() - t0:.0f} s)", flush=True)
+                rev_d[s] = _spike_loss_gate("from the plan's state", s, got[-1], lr_,
+                                            bf16_pipeline_loss(w_s, x, lab))
+            elif s < 6 or s % 10 == 0:
+                print(f"step {s}: oracle {want[s]:.5f} bf16 {got[-1]:.5f} ({time.time() - t0:.0f} s)", flush=True)
     d = [abs(g - w) / abs(w) for g, w in zip(got, want)]
-    i = int(np.argmax(d))
-    late = max(d[10:])
-    print(f"100-step trajectory: max rel diff {d[i]:.2e} at step {i} (bound {bound[i]:.1e}); steps 10-99 "
-          f"{late:.2e}; final {want[-1]:.5f} vs {got[-1]:.5f}", flush=True)
+    off = [d[s] for s in range(mk.STEPS) if s not in SPIKE]
+    print(f"100-step trajectory: outside the spike max rel diff {max(off):.2e}; spike free-running "
+          f"{[round(d[s], 4) for s in SPIKE]}, from the plan's own state (vs restatement, vs oracle) "
+          f"{[(f'{rev_d[s][0]:.1e}', f'{rev_d[s][1]:.1e}') for s in SPIKE]}; "
+          f"final {want[-1]:.5f} vs {got[-1]:.5f}", flush=True)
     for s in range(mk.STEPS):
-        assert d[s] <= bound[s], (s, got[s], want[s], bound[s])
-    assert late <= 2e-2
+        if s not in SPIKE:
+            assert d[s] <= 2e-2, (s, got[s], want[s])
+    assert max(d[10:]) <= 1e-3  # past the spike every implementation sits near ln(1000)
     assert not mlp.overflow()
 
 
@@ -227,8 +343,19 @@ def test_mixed_precision_overflow_skips_update(gpu, dims, batch):
 def test_linear4096_backward_bf16_full_size(gpu):
     """Linear 4096->4096 backward at batch 8192 (nn.rs:82-98 adjoints): X, dY
     ~N(0,1)/64 and Kaiming-uniform W in bf16; dX = dY·Wᵀ (bf16 out), dW = Xᵀ·dY
-    (f32 out) with db = colsum(dY) fused.  db is checked whole, dX and dW on
-    256 sampled entries each against float64 dot products."""
+    (f32 out) with db = colsum(dY) fused.  Every output entry is checked
+    against float64 GEMMs of the same bf16-rounded operands, with a bound per
+    entry from |A|·|B|:
+    * the products of two bf16 values are exact in f32, so the only error of
+      an f32-accumulated entry is summation rounding; it is far below
+      1e-5·Σ|a_k b_k| (its spread is ~4e-8 of that for these sums), while one
+      dropped or doubled term moves the entry by ~1/K of Σ|a_k b_k|
+      (1.2e-4 to 2.4e-4) and a wrong or zeroed tile by ~1/√K (1.1e-2 to
+      1.6e-2);
+    * dX is then rounded once to bf16 (round to nearest even): at most
+      2⁻⁸·|dX| more.
+    Then the whole outputs against the f32 inputs before rounding, within
+    2e-2 (norm-wise and max-relative)."""
     B, D = 8192, 4096
     rng = np.random.default_rng(33)
     x32 = rng.standard_normal((B, D), dtype=np.float32) / np.float32(64)
@@ -241,28 +368,32 @@ def test_linear4096_backward_bf16_full_size(gpu):
     gpu.gemm(G.NT, gdy, gw, dx)
     gpu.gemm(G.TN, gx, gdy, dw, colsum=db)
     got_dx, got_dw, got_db = gpu.download_f32(dx), gpu.download(dw), gpu.download(db)
-    x, dy, w = bf16_round(x32), bf16_round(dy32), bf16_round(w32)
-    # db whole, against the exact column sums of the rounded dY; f32
-    # accumulation stays far inside 1e-5 of the sum of magnitudes.
-    ex_b = dy.sum(0, keepdims=True, dtype=np.float64)
-    ab_b = np.abs(dy).sum(0, keepdims=True, dtype=np.float64)
-    assert np.all(np.abs(got_db - ex_b) <= 1e-5 * ab_b)
-    i, j = rng.integers(0, B, 256), rng.integers(0, D, 256)  # dX entries
-    p, q = rng.integers(0, D, 256), rng.integers(0, D, 256)  # dW entries
-    a_dx, b_dx = dy[i].astype(np.float64), w[j].astype(np.float64)
-    a_dw, b_dw = x[:, p].astype(np.float64), dy[:, q].astype(np.float64)
-    ex_dx, ab_dx = (a_dx * b_dx).sum(1), np.abs(a_dx * b_dx).sum(1)
-    ex_dw, ab_dw = (a_dw * b_dw).sum(0), np.abs(a_dw * b_dw).sum(0)
-    g_dx, g_dw = got_dx[i, j].astype(np.float64), got_dw[p, q].astype(np.float64)
-    # Same rounded operands: f32 accumulation, plus one bf16 rounding of dX.
-    assert np.all(np.abs(g_dw - ex_dw) <= 1e-5 * ab_dw)
-    assert np.all(np.abs(g_dx - ex_dx) <= 2.0 ** -8 * np.abs(ex_dx) + 1e-5 * ab_dx)
-    # Against the f32 inputs before rounding: within 2e-2.
-    f_dx = (dy32[i].astype(np.float64) * w32[j].astype(np.float64)).sum(1)
-    f_dw = (x32[:, p].astype(np.float64) * dy32[:, q].astype(np.float64)).sum(0)
-    # Scale-aware (a zeroed or wrong result scores ~1): max-relative and
-    # norm-wise over the samples, and for db over the whole vector.
-    f_db = dy32.sum(0, keepdims=True, dtype=np.float64)
-    rows = grad_gate("c3 vs the f32 inputs (dX, dW samples; db)", [f_dx, f_dw, f_db],
-                     [g_dx, g_dw, got_db.astype(np.float64)], 2e-2, 2e-2)
-    print(f"vs f32 inputs: dX {rows[0][1]:.2e}, dW {rows[1][1]:.2e} max-relative", flush=True)
+    del gx, gdy, gw, dx, dw, db
+    t0 = time.time()
+    x, dy, w = (bf16_round(a).astype(np.float64) for a in (x32, dy32, w32))
+    # db whole, against the exact column sums of the rounded dY
+    ex_b = dy.sum(0, keepdims=True)
+    assert np.all(np.abs(got_db - ex_b) <= 1e-5 * np.abs(dy).sum(0, keepdims=True))
+    # dW whole: K = 8192
+    ex = x.T @ dy
+    ab = np.abs(x).T @ np.abs(dy)
+    r_dw = np.abs(got_dw - ex) / ab
+    print(f"dW [{D},{D}] whole: max |err|/Σ|ab| {r_dw.max():.2e}, mean {r_dw.mean():.2e} "
+          f"({time.time() - t0:.0f} s)", flush=True)
+    assert np.all(np.abs(got_dw - ex) <= 1e-5 * ab)
+    del ex, ab, r_dw
+    # dX whole: K = 4096, then one bf16 rounding
+    ex = dy @ w.T
+    ab = np.abs(dy) @ np.abs(w).T
+    r_dx = np.abs(got_dx - ex) / (2.0 ** -8 * np.abs(ex) + 1e-5 * ab)
+    print(f"dX [{B},{D}] whole: max |err|/bound {r_dx.max():.3f} ({time.time() - t0:.0f} s)", flush=True)
+    assert np.all(np.abs(got_dx - ex) <= 2.0 ** -8 * np.abs(ex) + 1e-5 * ab)
+    del ex, ab, r_dx, x, dy, w
+    # Against the f32 inputs before rounding, whole, scale-aware (a zeroed or
+    # wrong result scores ~1 on both measures).
+    x, dy, w = (a.astype(np.float64) for a in (x32, dy32, w32))
+    f_dx, f_dw, f_db = dy @ w.T, x.T @ dy, dy.sum(0, keepdims=True)
+    rows = grad_gate("c3 vs the f32 inputs (dX, dW, db whole)", [f_dx, f_dw, f_db],
+                     [got_dx, got_dw, got_db], 2e-2, 2e-2)
+    print(f"vs f32 inputs: dX {rows[0][1]:.2e}, dW {rows[1][1]:.2e} max-relative ({time.time() - t0:.0f} s)",
+          flush=True)
