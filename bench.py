@@ -86,15 +86,22 @@ def label_flops(label, dims, batch):
     return 0
 
 
-def traffic_for(label):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
-    from the committed summary profiles/pmc_traffic.json, if present."""
+def traffic_for(label, section=None, key="bytes_per_launch"):
+    """HBM bytes measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by
+    a copy of known size) from the committed summary profiles/pmc_traffic.json,
+    if present: per launch of a batch-2048 step label, or under `section`
+    (small_batch: the batch-32 SGD step)."""
     path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(label, {}).get("bytes_per_launch")
+            doc = json.load(f)
     except (OSError, ValueError):
         return None
+    if section is not None:
+        doc = doc.get(section, {})
+    if label is None:
+        return doc.get(key)
+    return doc.get(label, {}).get(key)
 
 
 def bench_step(gpu, G, steps, warmup):
@@ -199,7 +206,12 @@ def bench_small(gpu, G, steps=2000, warmup=100):
             "launches_per_step": launches, "kernels_us": kern,
             "kernel_sum_us": round(sum(kern.values()), 2),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None, "bytes_per_step": byts,
+                         "frac": round(gbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic_for(None, "small_batch", "bytes_per_step"),
+                         "traffic_unit": "bytes per step (the 6 launches)",
+                         "traffic_source": "profiles/pmc_traffic.json small_batch: rocprofv3 --pmc FETCH_SIZE and "
+                                           "WRITE_SIZE of bench.py --only small, scaled by a copy kernel of known size",
+                         "bytes_per_step": byts,
                          "note": "a chain of dependent launches: the step is bound by launch latency, "
                                  "not by these bytes"},
             "vs_published": {"ref_gpu_ms": 0.73, "ref_cpu_ms": 14.01,
@@ -680,7 +692,12 @@ def main():
     if args.only in ("small", "bwd", "splitk", "colsum", "mixed", "copy", "tape", "pcie"):
         fn = {"small": bench_small, "bwd": bench_bwd_gemm, "splitk": bench_splitk, "colsum": bench_colsum,
               "mixed": bench_mixed, "copy": bench_copy, "tape": bench_tape, "pcie": bench_pcie}[args.only]
-        res = fn(gpu, G, rounds=args.rounds) if args.only == "bwd" else fn(gpu, G)
+        if args.only == "bwd":
+            res = fn(gpu, G, rounds=args.rounds)
+        elif args.only == "small" and (args.steps, args.warmup) != (500, 200):  # explicit: a short leg for counters
+            res = fn(gpu, G, steps=args.steps, warmup=args.warmup)
+        else:
+            res = fn(gpu, G)
         print(json.dumps({args.only: res}), flush=True)
         return
     wall, loss, prof, launches, settle = bench_step(gpu, G, args.steps, args.warmup)
