@@ -654,6 +654,7 @@ int rt_colsum(rt_ctx* c, const rt_buf* src, rt_buf* dst) {
   size_t R = src->shape[0], Cc = src->shape[1];
   if (dst->dtype != RT_F32 || dst->n != Cc) return fail(c, RT_ERR_SHAPE, "colsum target must be f32 [1,%zu]", Cc);
   if (src->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "colsum of u32");
+  if (R > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "colsum source too large");
   int rc = ensure_scratch(c, colsum_scratch_elems((int)R, (int)Cc, src->dtype));
   if (rc) return rc;
   Launch L(c, "colsum");
@@ -670,6 +671,7 @@ int rt_bias_add(rt_ctx* c, rt_buf* z, const rt_buf* b) {
   size_t cols = cols_of(z);
   if (b->n != cols || z->n % std::max<size_t>(cols, 1)) return fail(c, RT_ERR_SHAPE, "bias must have %zu elements", cols);
   if (z->n == 0) return RT_OK;
+  if (cols > (size_t)INT32_MAX || z->n / cols > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "bias_add: too large");
   Launch L(c, "bias_add");
   HIP_TRY(c, bias_add_launch(c->stream, static_cast<float*>(z->ptr), static_cast<const float*>(b->ptr),
                              (int)(z->n / cols), (int)cols),
@@ -708,6 +710,7 @@ int rt_softmax_xent(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, rt_bu
   if (delta->dtype != RT_F32 || delta->n != B * Cc) return fail(c, RT_ERR_SHAPE, "delta must be f32 [%zu,%zu]", B, Cc);
   if (loss_rows->dtype != RT_F32 || loss_rows->n != B) return fail(c, RT_ERR_SHAPE, "loss_rows must be f32 [%zu]", B);
   if (Cc == 0) return fail(c, RT_ERR_SHAPE, "zero classes");
+  if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "softmax_xent: too large");
   if (B == 0) return RT_OK;
   Launch L(c, "softmax_xent");
   HIP_TRY(c,

@@ -407,6 +407,22 @@ def test_shape_errors_are_reported(gpu):
     assert e.value.status == "RT_ERR_SHAPE"
 
 
+def test_row_counts_past_int32_are_refused(gpu):
+    # The row kernels take int row and column counts: 2^31 rows must be refused
+    # on the host, before any launch (8 GiB buffers, never initialised or read).
+    rows = 2 ** 31
+    z = gpu.empty((rows, 1))
+    lab = gpu.empty((rows,), G.U32)
+    calls = (lambda: gpu.colsum(z, gpu.zeros((1, 1))),
+             lambda: gpu.bias_add(z, gpu.zeros((1,))),
+             lambda: gpu.softmax_xent(z, lab, z, z))
+    for call in calls:
+        with pytest.raises(G.RtError) as e:
+            call()
+        assert e.value.status == "RT_ERR_SHAPE" and "large" in str(e.value)
+    del z, lab
+
+
 @pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (4100, 4000, 96)])
 @pytest.mark.parametrize("dt", [G.BF16, G.F16])
 def test_half_gemm_large_tiles(gpu, m, n, k, dt):
