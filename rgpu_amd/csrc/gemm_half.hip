@@ -70,17 +70,23 @@ struct HalfArgs {
   int vec_a, vec_b;
   int n_ragged;  // N is not a multiple of BN: B tiles read past column N, stores and sums stop at N
   int* nf_flag;  // non-null: set to 1 if any f32 result (C or column sums) is not finite
+  // ReLU predicate bits (GemmDesc::relu_bits_out / relu_bits): written by a
+  // bf16 bias+ReLU epilogue, read by the ReLU-mask epilogue instead of mask.
+  unsigned* relu_bits_out;
+  const unsigned* relu_bits;
 };
 
 __device__ inline int not_finite(float v) { return !(fabsf(v) <= 3.402823466e38f); }
 
 __device__ inline float bf16_to_f32(unsigned short h) { return __uint_as_float((unsigned int)h << 16); }
 
+// Round to nearest even; a NaN keeps its sign and top payload bits and is
+// made quiet.  Both results are computed and one selected (no branch).
 __device__ inline unsigned short f32_to_bf16_rne(float x) {
-  unsigned int u = __float_as_uint(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (unsigned short)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (unsigned short)(u >> 16);
+  const unsigned int u = __float_as_uint(x);
+  const unsigned int rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const unsigned int nan = (u >> 16) | 0x40u;
+  return (unsigned short)((u & 0x7fffffffu) > 0x7f800000u ? nan : rne);
 }
 
 template <bool IS_BF16>
@@ -472,10 +478,42 @@ __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[
                                              int wn, int g, int r, int slice) {
   float* Cf = static_cast<float*>(p.C) + (gridDim.z > 1 ? (long long)slice * p.split_stride : 0);
   unsigned short* Ch = static_cast<unsigned short*>(p.C);
+  // ReLU predicate bits (layout in rt_internal.h): this lane's dword of the
+  // 16-row x 64-column group of row block t, the byte of its 16x16 block
+  // u = 0 and, within the byte, the nibble of lane 16g + r.
+  static_assert(TN == 2 || TN == 4, "a wave tile spans half or all of a 64-column group");
+  const int lane = 16 * g + r, byte0 = (wn & 63) >> 4;
+  auto bits_dword = [&](int t) {
+    return 32 * ((long long)((m0 + wm) / 16 + t) * (p.N / 64) + (n0 + wn) / 64) + (lane >> 1);
+  };
+  // Loads the stores do not feed, issued before the first store (the
+  // compiler cannot move a load past a store it might alias, and each wait
+  // for a load also waits for every store before it): the bias of the wave
+  // tile's TN column groups, the same for all its rows, and the ReLU mask
+  // bits of its rows.
+  f4 bias[TN];
+  unsigned mbits[TM];
+#pragma unroll
+  for (int u = 0; u < TN; ++u) bias[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < TM; ++t) mbits[t] = 0;
+  if constexpr (EPI == RT_EPI_BIAS || EPI == RT_EPI_BIAS_RELU) {
+#pragma unroll
+    for (int u = 0; u < TN; ++u) {
+      const int col = n0 + wn + 16 * u + 4 * g;
+      if (!(p.n_ragged && col >= p.N)) bias[u] = *reinterpret_cast<const f4*>(p.bias + col);
+    }
+  } else if constexpr (EPI == RT_EPI_RELU_MASK) {
+    if (p.relu_bits) {
+#pragma unroll
+      for (int t = 0; t < TM; ++t) mbits[t] = p.relu_bits[bits_dword(t)] >> (4 * (lane & 1));
+    }
+  }
   int bad = 0;
 #pragma unroll
   for (int t = 0; t < TM; ++t) {
     const long long row_off = (long long)(m0 + wm + 16 * t + r) * p.ldc;
+    unsigned bits_w = 0;  // bias+ReLU with bits: this lane's and its neighbour's nibbles, by block
 #pragma unroll
     for (int u = 0; u < TN; ++u) {
       const int col = n0 + wn + 16 * u + 4 * g;
@@ -483,33 +521,62 @@ __device__ __forceinline__ void store_direct(const HalfArgs& p, const f4 (&acc)[
       const long long off = row_off + col;
       f4 v = acc[t][u];
       if constexpr (EPI == RT_EPI_BIAS || EPI == RT_EPI_BIAS_RELU) {
-        const f4 b = *reinterpret_cast<const f4*>(p.bias + col);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = v[e] + b[e];
+          v[e] = v[e] + bias[u][e];
           if constexpr (EPI == RT_EPI_BIAS_RELU) v[e] = fmaxf(v[e], 0.0f);
         }
       } else if constexpr (EPI == RT_EPI_RELU_MASK) {
-        f4 mk;
-        if (p.mask_bf16) {
-          const u2 h = *reinterpret_cast<const u2*>(static_cast<const unsigned short*>(p.mask) + off);
-          mk = f4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
-                  __uint_as_float(h[1] & 0xffff0000u)};
-        } else {
-          mk = *reinterpret_cast<const f4*>(static_cast<const float*>(p.mask) + off);
-        }
+        if (p.relu_bits) {
+          const unsigned nib = mbits[t] >> (8 * (byte0 + u));  // bit e: column 4g + e
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (!(mk[e] > 0.0f)) v[e] = 0.0f;
+          for (int e = 0; e < 4; ++e)
+            if (!((nib >> e) & 1u)) v[e] = 0.0f;
+        } else {
+          f4 mk;
+          if (p.mask_bf16) {
+            const u2 h = *reinterpret_cast<const u2*>(static_cast<const unsigned short*>(p.mask) + off);
+            mk = f4{__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u), __uint_as_float(h[1] << 16),
+                    __uint_as_float(h[1] & 0xffff0000u)};
+          } else {
+            mk = *reinterpret_cast<const f4*>(static_cast<const float*>(p.mask) + off);
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (!(mk[e] > 0.0f)) v[e] = 0.0f;
+        }
       }
       if constexpr (OUT_BF16) {
         u2 w;
         w[0] = (unsigned)f32_to_bf16_rne(v[0]) | ((unsigned)f32_to_bf16_rne(v[1]) << 16);
         w[1] = (unsigned)f32_to_bf16_rne(v[2]) | ((unsigned)f32_to_bf16_rne(v[3]) << 16);
         *reinterpret_cast<u2*>(Ch + off) = w;
+        if constexpr (EPI == RT_EPI_BIAS_RELU) {
+          if (p.relu_bits_out) {
+            // The predicate the mask epilogue applies to the stored bf16
+            // values (> 0) as a nibble, paired with the neighbour lane's
+            // (DPP quad_perm [1,0,3,2]) into one byte.
+            const unsigned nib = (unsigned)(__uint_as_float(w[0] << 16) > 0.0f) |
+                                 ((unsigned)(__uint_as_float(w[0] & 0xffff0000u) > 0.0f) << 1) |
+                                 ((unsigned)(__uint_as_float(w[1] << 16) > 0.0f) << 2) |
+                                 ((unsigned)(__uint_as_float(w[1] & 0xffff0000u) > 0.0f) << 3);
+            const unsigned other = (unsigned)__builtin_amdgcn_update_dpp(0, (int)nib, 0xB1, 0xF, 0xF, false);
+            bits_w |= ((lane & 1) ? other | (nib << 4) : nib | (other << 4)) << (8 * (byte0 + u));
+          }
+        }
       } else {
         *reinterpret_cast<f4*>(Cf + off) = v;
         bad |= not_finite(v[0]) | not_finite(v[1]) | not_finite(v[2]) | not_finite(v[3]);
+      }
+    }
+    if constexpr (EPI == RT_EPI_BIAS_RELU && OUT_BF16) {
+      // Even lanes store the pair's bytes: 128 (or 64) contiguous bytes.
+      if (p.relu_bits_out && !(lane & 1)) {
+        if constexpr (TN == 4)
+          p.relu_bits_out[bits_dword(t)] = bits_w;
+        else
+          reinterpret_cast<unsigned short*>(p.relu_bits_out + bits_dword(t))[byte0 >> 1] =
+              (unsigned short)(bits_w >> (8 * byte0));
       }
     }
   }
@@ -865,6 +932,11 @@ hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* 
   const HalfPath hp = pick_path<A_KC, B_KC>(a, splits, overread_ok);
   a.n_ragged = hp.dma && a.N % hp.tile != 0;
   if (!hp.dma || splits > 1) a.nf_flag = nullptr;  // gemm_checks_nonfinite says false for these
+  // Predicate bits only where the direct epilogue writes or reads them
+  // (gemm_relu_bits_ok): never leave them unwritten or ignored silently.
+  if ((a.relu_bits_out || a.relu_bits) &&
+      (!hp.dma || splits > 1 || a.n_ragged || a.M % 16 != 0 || a.N % 64 != 0))
+    return hipErrorInvalidValue;
   switch (hp.tile) {
     case 256:
       return hp.dma ? launch_dma<256, 256, 2, 4, A_KC, B_KC>(s, a, splits, bf16, cs_scratch, cs_elems,
@@ -921,6 +993,8 @@ static HalfArgs half_args(const GemmDesc& d, int splits) {
   a.vec_a = (d.lda % 8 == 0) && al16(d.A);
   a.vec_b = (d.ldb % 8 == 0) && al16(d.B);
   a.nf_flag = d.nf_flag;
+  a.relu_bits_out = d.epi == RT_EPI_BIAS_RELU && a.out_bf16 ? d.relu_bits_out : nullptr;
+  a.relu_bits = d.epi == RT_EPI_RELU_MASK ? d.relu_bits : nullptr;
   return a;
 }
 
@@ -941,6 +1015,20 @@ hipError_t gemm_half_launch(hipStream_t s, const GemmDesc& d) {
                                      d.cs_shares_to_caller);
   }
   return hipErrorInvalidValue;
+}
+
+bool gemm_relu_bits_ok(const GemmDesc& d) {
+  if ((d.in_dtype != RT_BF16 && d.in_dtype != RT_F16) || d.splits > 1 || d.M % 16 != 0 || d.N % 64 != 0) return false;
+  if (!(d.epi == RT_EPI_BIAS_RELU && d.out_dtype == RT_BF16) && d.epi != RT_EPI_RELU_MASK) return false;
+  const HalfArgs a = half_args(d, 1);
+  HalfPath hp{};
+  switch (d.layout) {
+    case RT_NN: hp = pick_path<true, false>(a, 1, d.overread_ok); break;
+    case RT_TN: hp = pick_path<false, false>(a, 1, d.overread_ok); break;
+    case RT_NT: hp = pick_path<true, true>(a, 1, d.overread_ok); break;
+    default: return false;
+  }
+  return hp.dma && a.N % hp.tile == 0;
 }
 
 bool gemm_checks_nonfinite(const GemmDesc& d) {

@@ -64,6 +64,12 @@ struct Layer {
   // region; the split reduction or the non-finite check launch adds them).
   float* cs_shares = nullptr;
   size_t cs_share_elems = 0;
+  // Mixed plans, hidden layers: the ReLU predicate of act as one bit per
+  // element (GemmDesc::relu_bits_out), written by the forward GEMM when its
+  // launch can (bits_fresh) and read by the next layer's dX GEMM in place of
+  // act's 16-bit values.
+  unsigned* relu_bits = nullptr;
+  bool bits_fresh = false;
   std::string lbl_fwd, lbl_fwd_red, lbl_dw, lbl_dw_red, lbl_dx, lbl_dx_red, lbl_bwd;
 };
 
@@ -194,10 +200,16 @@ static int finish_split(rt_mlp* p, const GemmDesc& d, const char* lbl_red, void*
 // Run one GEMM of the plan, with optional split-K.
 static int plan_gemm(rt_mlp* p, const char* lbl, const char* lbl_red, int layout, int in_dtype, const void* A,
                      const void* B, void* C, int out_dtype, int M, int N, int K, int lda, int ldb, int epi,
-                     const float* bias, const void* mask, int mask_dtype, float* colsum, int splits) {
+                     const float* bias, const void* mask, int mask_dtype, float* colsum, int splits,
+                     unsigned* relu_bits_out = nullptr, bool* bits_written = nullptr) {
   rt_ctx* c = p->ctx;
-  const GemmDesc d = plan_desc(p, layout, in_dtype, A, B, C, out_dtype, M, N, K, lda, ldb, epi, bias, mask,
-                               mask_dtype, colsum, splits);
+  GemmDesc d = plan_desc(p, layout, in_dtype, A, B, C, out_dtype, M, N, K, lda, ldb, epi, bias, mask, mask_dtype,
+                         colsum, splits);
+  if (relu_bits_out != nullptr) {
+    d.relu_bits_out = relu_bits_out;
+    if (!gemm_relu_bits_ok(d)) d.relu_bits_out = nullptr;
+    *bits_written = d.relu_bits_out != nullptr;
+  }
   {
     Launch Lz(c, lbl);
     hipError_t e = gemm_launch(c->stream, d);
@@ -230,9 +242,10 @@ static int run_forward(rt_mlp* p, const rt_buf* x, const rt_buf* labels, float s
     }
     const void* W = p->mixed ? (const void*)((unsigned short*)p->theta_h + Ly.w_off) : (const void*)(p->theta + Ly.w_off);
     const int out_dtype = (p->mixed && !last) ? RT_BF16 : RT_F32;
+    Ly.bits_fresh = false;
     int rc = plan_gemm(p, Ly.lbl_fwd.c_str(), Ly.lbl_fwd_red.c_str(), RT_NN, in_dtype, in, W, Ly.act, out_dtype, B,
                        (int)Ly.dout, (int)Ly.din, (int)Ly.din, (int)Ly.dout, last ? RT_EPI_BIAS : RT_EPI_BIAS_RELU,
-                       bias, nullptr, RT_F32, nullptr, Ly.splits_fwd);
+                       bias, nullptr, RT_F32, nullptr, Ly.splits_fwd, Ly.relu_bits, &Ly.bits_fresh);
     if (rc) return rc;
   }
   if (labels != nullptr) {
@@ -530,13 +543,16 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
   size_t o_theta = reserve(p->n_params * 4), o_grad = reserve(p->n_params * 4), o_m = reserve(p->n_params * 4),
          o_v = reserve(p->n_params * 4);
   size_t o_theta_h = p->mixed ? reserve(p->n_params * 2) : 0;
-  std::vector<size_t> o_act(n_layers), o_delta(n_layers), o_delta_h(n_layers);
+  std::vector<size_t> o_act(n_layers), o_delta(n_layers), o_delta_h(n_layers), o_bits(n_layers, 0);
+  std::vector<char> has_bits(n_layers, 0);
   for (int l = 0; l < n_layers; ++l) {
     const bool last = l == n_layers - 1;
     size_t elems = batch * p->L[l].dout;
     o_act[l] = reserve(elems * ((p->mixed && !last) ? 2 : 4));
     o_delta[l] = reserve(elems * 4);
     o_delta_h[l] = p->mixed ? reserve(batch * p->L[l].ldh * 2) : 0;
+    has_bits[l] = p->mixed && !last && batch % 16 == 0 && p->L[l].dout % 64 == 0;
+    if (has_bits[l]) o_bits[l] = reserve(elems / 8);
   }
   size_t o_part = reserve(part * 4);
   std::vector<size_t> o_dw_part(n_layers, 0);
@@ -563,6 +579,7 @@ int rt_mlp_create(rt_ctx* c, int n_layers, const size_t* dims, const float* cons
     p->L[l].act = p->arena + o_act[l];
     p->L[l].delta = (float*)(p->arena + o_delta[l]);
     p->L[l].delta_h = p->mixed ? (void*)(p->arena + o_delta_h[l]) : nullptr;
+    p->L[l].relu_bits = has_bits[l] ? (unsigned*)(p->arena + o_bits[l]) : nullptr;
   }
   p->partials = part ? (float*)(p->arena + o_part) : nullptr;
   for (int l = 0; l < n_layers; ++l) p->L[l].dw_parts = dw_part_elems[l] ? (float*)(p->arena + o_dw_part[l]) : nullptr;
@@ -769,9 +786,13 @@ int rt_mlp_step(rt_mlp* p, const rt_buf* x, const rt_buf* labels) {
       // With a padded δ_l (ld_dl > dout) K runs over the zero padding too:
       // those k read W's next row (finite weights) times zero.
       void* dst = p->mixed ? Lp.delta_h : (void*)Lp.delta;
-      const GemmDesc dx = plan_desc(p, RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B, (int)Ly.din,
-                                    ld_dl, ld_dl, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act,
-                                    p->mixed ? RT_BF16 : RT_F32, nullptr, Ly.splits_dx);
+      GemmDesc dx = plan_desc(p, RT_NT, in_dtype, dl, W, dst, p->mixed ? RT_BF16 : RT_F32, B, (int)Ly.din, ld_dl,
+                              ld_dl, (int)Ly.dout, RT_EPI_RELU_MASK, nullptr, Lp.act, p->mixed ? RT_BF16 : RT_F32,
+                              nullptr, Ly.splits_dx);
+      if (Lp.bits_fresh) {  // the same predicate, 1/16 of the bytes
+        dx.relu_bits = Lp.relu_bits;
+        if (!gemm_relu_bits_ok(dx)) dx.relu_bits = nullptr;
+      }
       if (Ly.pair_bwd) {
         // Both read δ_l and neither feeds the other: one launch.
         Launch Lz(c, Ly.lbl_bwd.c_str());

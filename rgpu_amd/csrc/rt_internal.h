@@ -181,8 +181,22 @@ struct GemmDesc {
   // Optional: set *nf_flag = 1 if any f32 result is not finite.  Honoured
   // only where gemm_checks_nonfinite(d) is true.
   int* nf_flag = nullptr;
+  // Optional ReLU predicate bits, one per element of C: a bf16 bias+ReLU
+  // launch writes them (relu_bits_out: bit set where the stored value is
+  // > 0), a ReLU-mask launch reads them instead of `mask` (relu_bits), 1/16
+  // of a bf16 mask's bytes.  Layout, in the direct epilogue's lane order:
+  // rows 16R.. and columns 64G.. of C are the 32 dwords from 32·(R·N/64 +
+  // G); byte b of dword j covers the 16x16 block of columns 64G + 16b, and
+  // its low / high nibble lane 2j / 2j + 1, where lane L stands for row
+  // 16R + L%16 and columns 4·(L/16) + q, q = 0..3 the nibble's bits.  A
+  // launch that sets either pointer must satisfy gemm_relu_bits_ok(d)
+  // (whole tiles, M % 16 == 0, N % 64 == 0); otherwise it fails rather than
+  // ignore them.
+  unsigned* relu_bits_out = nullptr;
+  const unsigned* relu_bits = nullptr;
 };
 bool gemm_checks_nonfinite(const GemmDesc& d);
+bool gemm_relu_bits_ok(const GemmDesc& d);
 // Narrow f32 NN products (<= 16 columns) go to the output-layer kernel, in
 // rt_gemm and in a one-slice split-K alike.
 bool narrow_nn(const GemmDesc& d);

@@ -340,6 +340,33 @@ def test_mixed_precision_overflow_skips_update(gpu, dims, batch):
     assert any(not np.array_equal(a, b) for a, b in zip(w0, mlp.weights()))
 
 
+@pytest.mark.parametrize("dims,batch", [([256, 512, 512, 256, 64], 256), ([1024, 4096, 4096, 64], 4096)])
+def test_mixed_plan_dx_equals_the_activation_masked_gemm(gpu, dims, batch):
+    # The bf16 plan's dX GEMMs take the ReLU predicate as one bit per element,
+    # written by the forward GEMM (64x64 tiles at the first shape, 256x256 at
+    # the second).  Each δ_{l-1} must be, bit for bit, the standalone NT GEMM
+    # masked by the stored bf16 activation A_{l-1}, on the plan's own δ_l and
+    # the bf16 weights the step started from.
+    params = kaiming_model(31, dims)
+    x = normal_batch(32, batch, dims[0])
+    lab = uniform_labels(33, batch, dims[-1])
+    mlp = G.GpuMlp.from_params(gpu, params, batch, 1e-3, precision="bf16", loss_scale=1024.0)
+    mlp.step(gpu.upload(x, G.BF16), G.upload_labels(gpu, lab))
+    assert not mlp.overflow()
+    zeros = 0
+    for l in range(len(dims) - 2, 0, -1):
+        act = mlp.activation(l - 1)
+        zeros += int((act == 0).sum())
+        d = gpu.upload(mlp.delta(l), G.BF16)
+        w = gpu.upload(params[2 * l], G.BF16)
+        out = gpu.zeros((batch, dims[l]), G.BF16)
+        gpu.gemm(G.NT, d, w, out, G.EPI_RELU_MASK, gpu.upload(act, G.BF16))
+        want = G.f32_to_bf16_bits(gpu.download_f32(out))
+        got = G.f32_to_bf16_bits(mlp.delta(l - 1))
+        assert np.array_equal(got, want), (l, int((got != want).sum()))
+    assert zeros > 0  # the masks are not all ones
+
+
 def test_linear4096_backward_bf16_full_size(gpu):
     """Linear 4096->4096 backward at batch 8192 (nn.rs:82-98 adjoints): X, dY
     ~N(0,1)/64 and Kaiming-uniform W in bf16; dX = dY·Wᵀ (bf16 out), dW = Xᵀ·dY
