@@ -935,7 +935,8 @@ hipError_t launch_half(hipStream_t s, HalfArgs a, int splits, bool bf16, float* 
   // Predicate bits only where the direct epilogue writes or reads them
   // (gemm_relu_bits_ok): never leave them unwritten or ignored silently.
   if ((a.relu_bits_out || a.relu_bits) &&
-      (!hp.dma || splits > 1 || a.n_ragged || a.M % 16 != 0 || a.N % 64 != 0))
+      (!hp.dma || splits > 1 || a.n_ragged || a.M % 16 != 0 || a.N % 64 != 0 ||
+       (a.relu_bits_out && !(a.epi == RT_EPI_BIAS_RELU && a.out_bf16)) || (a.relu_bits && a.epi != RT_EPI_RELU_MASK)))
     return hipErrorInvalidValue;
   switch (hp.tile) {
     case 256:
@@ -993,8 +994,8 @@ static HalfArgs half_args(const GemmDesc& d, int splits) {
   a.vec_a = (d.lda % 8 == 0) && al16(d.A);
   a.vec_b = (d.ldb % 8 == 0) && al16(d.B);
   a.nf_flag = d.nf_flag;
-  a.relu_bits_out = d.epi == RT_EPI_BIAS_RELU && a.out_bf16 ? d.relu_bits_out : nullptr;
-  a.relu_bits = d.epi == RT_EPI_RELU_MASK ? d.relu_bits : nullptr;
+  a.relu_bits_out = d.relu_bits_out;
+  a.relu_bits = d.relu_bits;
   return a;
 }
 
