@@ -335,13 +335,14 @@ def test_adam_and_sgd_are_bit_exact_with_cpu_arithmetic(gpu):
 def test_adam_launch_larger_than_the_cache_gives_the_same_bits(gpu):
     # An optimizer launch that moves more than the 256 MB last-level cache
     # reads and writes its streams non-temporally; the same update as two
-    # launches of half the size each does not.  Same arithmetic, same bits.
-    n, h = 10_000_000, 5_000_000  # 28 B per Adam parameter: ~280 MB, ~140 MB
+    # launches of half the size each does not.  Same arithmetic, same bits,
+    # the ragged tail (n not a multiple of 4) included.
+    n, h = 10_000_003, 5_000_000  # 28 B per Adam parameter: ~280 MB, ~140 MB
     rng = np.random.default_rng(21)
     theta = rng.normal(size=(1, n)).astype(np.float32)
     whole = [gpu.upload(theta), gpu.zeros((1, n)), gpu.zeros((1, n))]
-    parts = [[gpu.upload(np.ascontiguousarray(theta[:, s])), gpu.zeros((1, h)), gpu.zeros((1, h))]
-             for s in (slice(0, h), slice(h, n))]
+    parts = [[gpu.upload(np.ascontiguousarray(theta[:, s])), gpu.zeros((1, w)), gpu.zeros((1, w))]
+             for s, w in ((slice(0, h), h), (slice(h, n), n - h))]
     for t in (1, 2, 3):
         g = (rng.normal(size=(1, n)) * 10.0 ** -t).astype(np.float32)
         gpu.adam(*whole, gpu.upload(g), 1e-3, (0.9, 0.999), t)
