@@ -100,6 +100,11 @@ using namespace rt;
 static std::string g_open_err;
 
 static bool is_half(rt_dtype d) { return d == RT_BF16 || d == RT_F16; }
+// Row and column counts of the row kernels (column sums, bias add, softmax
+// cross-entropy, argmax): their int row / column indices and launch plans
+// add a block's or a chunk's extent to a count, so counts stay well below
+// INT32_MAX.
+static constexpr size_t kRowOpMax = size_t(1) << 30;
 static size_t cols_of(const rt_buf* b) { return b->rank >= 2 ? b->shape[b->rank - 1] : b->n; }
 
 extern "C" {
@@ -658,7 +663,7 @@ int rt_colsum(rt_ctx* c, const rt_buf* src, rt_buf* dst) {
   size_t R = src->shape[0], Cc = src->shape[1];
   if (dst->dtype != RT_F32 || dst->n != Cc) return fail(c, RT_ERR_SHAPE, "colsum target must be f32 [1,%zu]", Cc);
   if (src->dtype == RT_U32) return fail(c, RT_ERR_DTYPE, "colsum of u32");
-  if (R > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "colsum source too large");
+  if (R > kRowOpMax || Cc > kRowOpMax) return fail(c, RT_ERR_SHAPE, "colsum source too large");
   int rc = ensure_scratch(c, colsum_scratch_elems((int)R, (int)Cc, src->dtype));
   if (rc) return rc;
   Launch L(c, "colsum");
@@ -675,7 +680,7 @@ int rt_bias_add(rt_ctx* c, rt_buf* z, const rt_buf* b) {
   size_t cols = cols_of(z);
   if (b->n != cols || z->n % std::max<size_t>(cols, 1)) return fail(c, RT_ERR_SHAPE, "bias must have %zu elements", cols);
   if (z->n == 0) return RT_OK;
-  if (cols > (size_t)INT32_MAX || z->n / cols > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "bias_add: too large");
+  if (cols > kRowOpMax || z->n / cols > kRowOpMax) return fail(c, RT_ERR_SHAPE, "bias_add: too large");
   Launch L(c, "bias_add");
   HIP_TRY(c, bias_add_launch(c->stream, static_cast<float*>(z->ptr), static_cast<const float*>(b->ptr),
                              (int)(z->n / cols), (int)cols),
@@ -714,7 +719,7 @@ int rt_softmax_xent(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, rt_bu
   if (delta->dtype != RT_F32 || delta->n != B * Cc) return fail(c, RT_ERR_SHAPE, "delta must be f32 [%zu,%zu]", B, Cc);
   if (loss_rows->dtype != RT_F32 || loss_rows->n != B) return fail(c, RT_ERR_SHAPE, "loss_rows must be f32 [%zu]", B);
   if (Cc == 0) return fail(c, RT_ERR_SHAPE, "zero classes");
-  if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "softmax_xent: too large");
+  if (B > kRowOpMax || Cc > kRowOpMax) return fail(c, RT_ERR_SHAPE, "softmax_xent: too large");
   if (B == 0) return RT_OK;
   Launch L(c, "softmax_xent");
   HIP_TRY(c,
@@ -732,7 +737,7 @@ int rt_argmax_rows(rt_ctx* c, const rt_buf* logits, rt_buf* out) {
   const size_t B = logits->shape[0], Cc = logits->shape[1];
   if (out->dtype != RT_U32 || out->n != B) return fail(c, RT_ERR_SHAPE, "out must be u32 [%zu]", B);
   if (Cc == 0 && B > 0) return fail(c, RT_ERR_SHAPE, "zero classes");
-  if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "too large");
+  if (B > kRowOpMax || Cc > kRowOpMax) return fail(c, RT_ERR_SHAPE, "argmax: too large");
   if (B == 0) return RT_OK;
   Launch L(c, "argmax");
   HIP_TRY(c,
@@ -754,7 +759,7 @@ int rt_accuracy(rt_ctx* c, const rt_buf* logits, const rt_buf* labels, float* ou
     *out = B == 0 ? std::nanf("") : 0.0f;
     return RT_OK;
   }
-  if (B > (size_t)INT32_MAX || Cc > (size_t)INT32_MAX) return fail(c, RT_ERR_SHAPE, "too large");
+  if (B > kRowOpMax || Cc > kRowOpMax) return fail(c, RT_ERR_SHAPE, "argmax: too large");
   // Predictions in the context scratch (grow-only), then compared on the host.
   int rc = ensure_scratch(c, B);
   if (rc) return rc;

@@ -329,7 +329,9 @@ template <int R>
 hipError_t binary_launch_r(hipStream_t s, int op, const float* a, const float* b, float* out, const Shape4& sh,
                            long long n) {
   const dim3 grid(grid_for(n)), block(256);
-  if (n < (1LL << 31))
+  // 32-bit indices only where the grid-stride index cannot pass INT32_MAX
+  // (its last step goes up to n - 1 + the grid's threads).
+  if (n <= (1LL << 31) - 1 - (long long)grid.x * 256)
     rt::launch((binary_kernel<R, int>), grid, block, 0, s, op, a, b, out, sh, (int)n);
   else
     rt::launch((binary_kernel<R, long long>), grid, block, 0, s, op, a, b, out, sh, n);

@@ -409,8 +409,9 @@ def test_shape_errors_are_reported(gpu):
 
 
 def test_row_counts_past_int32_are_refused(gpu):
-    # The row kernels take int row and column counts: 2^31 rows must be refused
-    # on the host, before any launch (8 GiB buffers, never initialised or read).
+    # The row kernels take int row and column counts and add block extents to
+    # them: counts above 2^30 are refused on the host, before any launch
+    # (8 GiB buffers of 2^31 rows, never initialised or read).
     rows = 2 ** 31
     z = gpu.empty((rows, 1))
     lab = gpu.empty((rows,), G.U32)
