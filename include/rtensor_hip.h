@@ -140,8 +140,8 @@ int rt_gemm_splitk_static(rt_ctx* ctx, rt_layout layout, const rt_buf* a, const 
 size_t rt_splitk_slices(size_t m, size_t n, size_t k);
 
 /* Row and column counts of rt_colsum, rt_bias_add, rt_softmax_xent,
- * rt_argmax_rows and rt_accuracy are at most 2^30 each (RT_ERR_SHAPE
- * otherwise). */
+ * rt_argmax_rows and rt_accuracy, and M, N, K of the GEMM entry points, are
+ * at most 2^30 each (RT_ERR_SHAPE otherwise). */
 /* ops_colsum (mod.rs:838-855): dst[1, C] (f32) = 1ᵀ·src[R, C] (f32/bf16/f16). */
 int rt_colsum(rt_ctx* ctx, const rt_buf* src, rt_buf* dst);
 /* op_bias_add (mod.rs:752-762): Z += 1ₙb in place. */

@@ -101,9 +101,9 @@ static std::string g_open_err;
 
 static bool is_half(rt_dtype d) { return d == RT_BF16 || d == RT_F16; }
 // Row and column counts of the row kernels (column sums, bias add, softmax
-// cross-entropy, argmax): their int row / column indices and launch plans
-// add a block's or a chunk's extent to a count, so counts stay well below
-// INT32_MAX.
+// cross-entropy, argmax) and GEMM dimensions: their int indices and launch
+// plans add a block's, tile's or chunk's extent to a count, so counts stay
+// well below INT32_MAX.
 static constexpr size_t kRowOpMax = size_t(1) << 30;
 static size_t cols_of(const rt_buf* b) { return b->rank >= 2 ? b->shape[b->rank - 1] : b->n; }
 
@@ -415,7 +415,8 @@ static int gemm_shapes(rt_ctx* c, rt_layout layout, const rt_buf* a, const rt_bu
     case RT_NT: *M = am; *K = ak; *N = bk; if (bn != ak) goto bad; break;   // B stored [N, K]
     default: return fail(c, RT_ERR_INVALID, "unknown layout %d", (int)layout);
   }
-  if (*M > 0x7fffffff || *N > 0x7fffffff || *K > 0x7fffffff) return fail(c, RT_ERR_SHAPE, "dimension too large");
+  // The kernels index tiles with int and round M, N, K up to whole tiles.
+  if (*M > kRowOpMax || *N > kRowOpMax || *K > kRowOpMax) return fail(c, RT_ERR_SHAPE, "dimension too large");
   return RT_OK;
 bad:
   return fail(c, RT_ERR_SHAPE, "gemm inner dimensions differ: [%zu,%zu] x [%zu,%zu] (layout %d)", am, ak, bk, bn,
@@ -503,7 +504,7 @@ int rt_linear_backward(rt_ctx* c, const rt_buf* x, const rt_buf* delta, const rt
   const bool f32 = x->dtype == RT_F32 && delta->dtype == RT_F32 && w->dtype == RT_F32;
   const bool outs_f32 = dw->dtype == RT_F32 && (!dx || dx->dtype == RT_F32) && (!db || db->dtype == RT_F32);
   if (f32 && outs_f32 && dx && dw->n == k * n && dx->n == m * k && (!db || db->n == n) && m && n && k &&
-      m <= INT32_MAX && n <= INT32_MAX && k <= INT32_MAX) {
+      m <= kRowOpMax && n <= kRowOpMax && k <= kRowOpMax) {
     GemmDesc d0;  // dW = Xᵀ·δ (+ db = 1ᵀδ)
     d0.layout = RT_TN;
     d0.A = x->ptr;
