@@ -340,13 +340,15 @@ def test_mixed_precision_overflow_skips_update(gpu, dims, batch):
     assert any(not np.array_equal(a, b) for a, b in zip(w0, mlp.weights()))
 
 
-@pytest.mark.parametrize("dims,batch", [([256, 512, 512, 256, 64], 256), ([1024, 4096, 4096, 64], 4096)])
+@pytest.mark.parametrize("dims,batch", [([256, 512, 512, 256, 64], 256), ([1024, 4096, 4096, 64], 4096),
+                                        ([256, 96, 160, 64], 200)])
 def test_mixed_plan_dx_equals_the_activation_masked_gemm(gpu, dims, batch):
     # The bf16 plan's dX GEMMs take the ReLU predicate as one bit per element,
     # written by the forward GEMM (64x64 tiles at the first shape, 256x256 at
-    # the second).  Each δ_{l-1} must be, bit for bit, the standalone NT GEMM
-    # masked by the stored bf16 activation A_{l-1}, on the plan's own δ_l and
-    # the bf16 weights the step started from.
+    # the second); at the third (widths not a multiple of 64, ragged rows)
+    # they read the activation itself.  Each δ_{l-1} must be, bit for bit, the
+    # standalone NT GEMM masked by the stored bf16 activation A_{l-1}, on the
+    # plan's own δ_l and the bf16 weights the step started from.
     params = kaiming_model(31, dims)
     x = normal_batch(32, batch, dims[0])
     lab = uniform_labels(33, batch, dims[-1])
