@@ -69,7 +69,8 @@ typedef enum {
 /* Gpu::new / Gpu::with_preference (mod.rs:263-277).  device = HIP ordinal. */
 int rt_open(int device, rt_ctx** out);
 int rt_close(rt_ctx* ctx);
-/* Message for the last failed call on ctx (or of rt_open when ctx is NULL). */
+/* Message for the last failed call on ctx (or, when ctx is NULL, of the
+ * calling thread's last failed rt_open). */
 const char* rt_last_error(const rt_ctx* ctx);
 /* Gpu::info (mod.rs:412): device name and arch, NUL-terminated into buf. */
 int rt_info(rt_ctx* ctx, char* buf, size_t len);

@@ -97,7 +97,9 @@ Launch::~Launch() {
 
 using namespace rt;
 
-static std::string g_open_err;
+// rt_open's last failure, per calling thread (contexts opened on different
+// threads do not share it).
+static thread_local std::string g_open_err;
 
 static bool is_half(rt_dtype d) { return d == RT_BF16 || d == RT_F16; }
 // Row and column counts of the row kernels (column sums, bias add, softmax
